@@ -1,0 +1,349 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one JSON line on stdout).
+
+Headline ("value"): flash_attention forward+backward at BASELINE config 3
+(bf16, causal, GQA, B=2, Hq=16, Hkv=4, S=8192, D=128) in algorithmic
+TFLOP/s: 4*B*Hq*D*S(S+1)/2 per forward, x3.5 for forward+backward
+(recomputation not credited). One step = one forward + backward over the
+resident synthetic batch: pf_attn_fwd, then pf_attn_bwd_delta,
+pf_attn_bwd_dq and pf_attn_bwd_dkv, called through the C ABI on torch's
+current stream with HIP events between the launches (per-kernel durations).
+
+Secondary figures in the same line (each timed with HIP events):
+  fwd_tflops    config 3 forward alone (the pf_attn_fwd launches of the steps)
+  rope_tflops   config 2 fused-RoPE prefill, bf16 causal GQA B=4 Hq=32 Hkv=8 S=4096
+  decode_gbs    config 4 decode, B=64 Hq=32 Hkv=8, cache 8192 with kv_len 6000
+                (slots past 6000 NaN); algorithmic bytes = valid K/V once + q + o
+  paged_gbs     config 5 paged decode, 128 seqs, page 64, lens U[512, 8192] from
+                np.random.default_rng(0), 16384-page pool, -1-padded table,
+                unreferenced pages and tails NaN; bytes = valid K/V + q + o +
+                used table entries + lens
+
+Synthetic inputs: N(0,1) from torch's CUDA generator seeded 0 (config 5's
+lengths and page permutation from numpy's default_rng(0)), cast to bf16.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "tpu-native-pallas-flashattention_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "attn TFLOP/s fwd & fwd+bwd at S=8K D=128; decode/paged HBM GB/s (1 GPU)"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def causal_pairs(S: int) -> int:
+    return S * (S + 1) // 2
+
+
+def fwd_flops(B, Hq, D, pairs) -> float:
+    return 4.0 * B * Hq * D * pairs
+
+
+class Events:
+    """Pairs of HIP events recorded on the current stream."""
+
+    def __init__(self, n_marks: int, n_iters: int):
+        import torch
+        self.ev = [[torch.cuda.Event(enable_timing=True) for _ in range(n_marks)] for _ in range(n_iters)]
+
+    def mark(self, it: int, j: int):
+        self.ev[it][j].record()
+
+    def mean_ms(self, j0: int, j1: int) -> float:
+        return float(np.mean([e[j0].elapsed_time(e[j1]) for e in self.ev]))
+
+
+def ok(status: int, what: str):
+    if status != 0:
+        raise RuntimeError(f"{what} failed with status {status}")
+
+
+def bench_cfg3(L, _lib, torch, steps, warmup):
+    B, Hq, Hkv, S, D = 2, 16, 4, 8192, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    mk = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+    q, k, v, do = mk(B, Hq, S, D), mk(B, Hkv, S, D), mk(B, Hkv, S, D), mk(B, Hq, S, D)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device="cuda")
+    delta = torch.empty_like(lse)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    scale = 1.0 / D ** 0.5
+    fa = _lib.FwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                      B, Hq, Hkv, S, S, D, S, 1, scale, 1)
+    ba = _lib.BwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                      lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                      B, Hq, Hkv, S, S, D, S, 1, scale, 1)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def step(ev=None, it=0):
+        if ev: ev.mark(it, 0)
+        ok(L.pf_attn_fwd(fa, st), "pf_attn_fwd")
+        if ev: ev.mark(it, 1)
+        ok(L.pf_attn_bwd_delta(ba, st), "pf_attn_bwd_delta")
+        if ev: ev.mark(it, 2)
+        ok(L.pf_attn_bwd_dq(ba, st), "pf_attn_bwd_dq")
+        if ev: ev.mark(it, 3)
+        ok(L.pf_attn_bwd_dkv(ba, st), "pf_attn_bwd_dkv")
+        if ev: ev.mark(it, 4)
+
+    for _ in range(warmup):
+        step()
+    ev = Events(5, steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(ev, i)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    kern_ms = {"pf_attn_fwd_kernel": ev.mean_ms(0, 1), "pf_attn_bwd_delta_kernel": ev.mean_ms(1, 2),
+               "pf_attn_bwd_dq_kernel": ev.mean_ms(2, 3), "pf_attn_bwd_dkv_kernel": ev.mean_ms(3, 4)}
+    F = fwd_flops(B, Hq, D, causal_pairs(S))
+    # algorithmic credit per launch: fwd = 2 matmuls; dkv = S, dP, dV, dK (4); dq = dQ (1)
+    credit = {"pf_attn_fwd_kernel": F, "pf_attn_bwd_dq_kernel": 0.5 * F, "pf_attn_bwd_dkv_kernel": 2.0 * F}
+    host = {"q": q, "k": k, "v": v, "do": do}
+    return dict(B=B, Hq=Hq, Hkv=Hkv, S=S, D=D, wall_ms=wall_ms, kern_ms=kern_ms, F=F, credit=credit,
+                host=host)
+
+
+def bench_rope(L, _lib, torch, iters):
+    from pallas_flash import precompute_rope
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    g = torch.Generator(device="cuda").manual_seed(1)
+    mk = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+    q, k, v = mk(B, Hq, S, D), mk(B, Hkv, S, D), mk(B, Hkv, S, D)
+    cos, sin = precompute_rope(S, D, 10000.0, device="cuda")
+    o = torch.empty_like(q)
+    base = _lib.FwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None,
+                        B, Hq, Hkv, S, S, D, S, 1, 1.0 / D ** 0.5, 1)
+    ra = _lib.FwdRopeArgs(base, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(), sin.data_ptr())
+    st = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        ok(L.pf_attn_fwd_rope(ra, st), "pf_attn_fwd_rope")
+    ev = Events(2, iters)
+    for i in range(iters):
+        ev.mark(i, 0)
+        ok(L.pf_attn_fwd_rope(ra, st), "pf_attn_fwd_rope")
+        ev.mark(i, 1)
+    torch.cuda.synchronize()
+    ms = ev.mean_ms(0, 1)
+    return ms, fwd_flops(B, Hq, D, causal_pairs(S))
+
+
+def _decode_args_and_ws(L, _lib, torch, args, size_fn):
+    ws_bytes = size_fn(args)
+    ws = torch.empty(max(int(ws_bytes), 256), dtype=torch.uint8, device="cuda")
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = ws.numel()
+    return ws
+
+
+def bench_decode(L, _lib, torch, iters):
+    B, Hq, Hkv, cap, D, kv_len = 64, 32, 8, 8192, 128, 6000
+    g = torch.Generator(device="cuda").manual_seed(2)
+    q = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    kc = torch.empty((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    for t in (kc, vc):
+        t[:, :, :kv_len].copy_(torch.randn((B, Hkv, kv_len, D), generator=g, device="cuda"))
+        t[:, :, kv_len:].fill_(float("nan"))
+    o = torch.empty_like(q)
+    args = _lib.DecodeArgs(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), B, Hq, Hkv, cap,
+                           D, kv_len, 1.0 / D ** 0.5, 1, None, 0)
+    ws = _decode_args_and_ws(L, _lib, torch, args, L.pf_attn_decode_workspace_size)
+    st = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        ok(L.pf_attn_decode(args, st), "pf_attn_decode")
+    ev = Events(2, iters)
+    for i in range(iters):
+        ev.mark(i, 0)
+        ok(L.pf_attn_decode(args, st), "pf_attn_decode")
+        ev.mark(i, 1)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all(), "decode output not finite"
+    nbytes = B * Hkv * kv_len * D * 2 * 2 + 2 * B * Hq * D * 2
+    del ws
+    return ev.mean_ms(0, 1), nbytes
+
+
+def bench_paged(L, _lib, torch, iters):
+    B, Hq, Hkv, D, page, npages, pps = 128, 32, 8, 128, 64, 16384, 128
+    rng = np.random.default_rng(0)
+    lens = rng.integers(512, 8193, B)
+    perm = rng.permutation(npages)
+    table = np.full((B, pps), -1, np.int32)
+    used = np.zeros(npages, bool)
+    cur = 0
+    for b in range(B):
+        n = -(-int(lens[b]) // page)
+        table[b, :n] = perm[cur:cur + n]
+        used[perm[cur:cur + n]] = True
+        cur += n
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    kp = torch.randn((npages, Hkv, page, D), generator=g, device="cuda").to(torch.bfloat16)
+    vp = torch.randn((npages, Hkv, page, D), generator=g, device="cuda").to(torch.bfloat16)
+    unused = torch.as_tensor(np.nonzero(~used)[0], device="cuda")
+    for t in (kp, vp):
+        t[unused] = float("nan")
+        for b in range(B):  # beyond-length tail of each sequence's last page
+            n = -(-int(lens[b]) // page)
+            tail = int(lens[b]) - (n - 1) * page
+            if tail < page:
+                t[int(table[b, n - 1]), :, tail:] = float("nan")
+    tt = torch.as_tensor(table, device="cuda")
+    tl = torch.as_tensor(lens.astype(np.int32), device="cuda")
+    o = torch.empty_like(q)
+    args = _lib.PagedArgs(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), tt.data_ptr(), tl.data_ptr(),
+                          o.data_ptr(), B, Hq, Hkv, npages, page, D, pps, 1.0 / D ** 0.5, 1, None, 0)
+    ws = _decode_args_and_ws(L, _lib, torch, args, L.pf_paged_attn_workspace_size)
+    st = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        ok(L.pf_paged_attn(args, st), "pf_paged_attn")
+    ev = Events(2, iters)
+    for i in range(iters):
+        ev.mark(i, 0)
+        ok(L.pf_paged_attn(args, st), "pf_paged_attn")
+        ev.mark(i, 1)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all(), "paged output not finite"
+    npg = -(-lens // page)
+    nbytes = int(lens.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2 + 4 * int(npg.sum()) + 4 * B
+    del ws
+    return ev.mean_ms(0, 1), nbytes
+
+
+def cpu_baseline(c3):
+    """The float32 numpy restatement of the reference algorithm (oracle/),
+    forward + backward on a bounded sample of config 3: batch 0, query heads
+    0-1 (which share KV head 0), full S=8192 causal. Credited FLOPs of the
+    sample / wall time."""
+    import torch
+    from oracle import attention_bwd_ref, attention_ref
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = 1
+    S, D = c3["S"], c3["D"]
+    h = c3["host"]
+    f32 = lambda t: t.float().cpu().numpy()
+    q = f32(h["q"][0:1, 0:2])
+    k = f32(h["k"][0:1, 0:1])
+    v = f32(h["v"][0:1, 0:1])
+    do = f32(h["do"][0:1, 0:2])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    attention_ref(q, k, v, causal=True, dtype=np.float32)
+    attention_bwd_ref(q, k, v, do, causal=True, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    flops = 3.5 * fwd_flops(1, 2, D, causal_pairs(S))
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"numpy float32 restatement (oracle/attention.py) of reference.py + its "
+                      f"backward, fwd+bwd of config 3 batch 0 heads 0-1 (2 of 32 heads) at "
+                      f"S={S}, {dt:.1f} s wall; BLAS threads={threads}, elementwise ops 1 thread"}
+
+
+def load_traffic(kernel: str, workload: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(workload, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged"], default="all")
+    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); see DESIGN.md for how the path would shard.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from pallas_flash import _lib
+    L = _lib.lib()
+    torch.cuda.set_device(0)
+    iters = max(args.steps, 5)
+    sec = {}
+
+    c3 = None
+    if args.only in ("all", "cfg3"):
+        log("cfg3 fwd+bwd ...")
+        c3 = bench_cfg3(L, _lib, torch, args.steps, args.warmup)
+        sec["fwd_tflops"] = c3["F"] / (c3["kern_ms"]["pf_attn_fwd_kernel"] * 1e-3) / 1e12
+        sec["kernel_ms"] = {k: round(v, 4) for k, v in c3["kern_ms"].items()}
+    if args.only in ("all", "rope"):
+        log("cfg2 rope ...")
+        ms, F = bench_rope(L, _lib, torch, iters)
+        sec["rope_tflops"] = F / (ms * 1e-3) / 1e12
+        sec["rope_ms"] = ms
+    if args.only in ("all", "decode"):
+        log("cfg4 decode ...")
+        ms, nb = bench_decode(L, _lib, torch, iters)
+        sec["decode_gbs"] = nb / (ms * 1e-3) / 1e9
+        sec["decode_ms"] = ms
+    if args.only in ("all", "paged"):
+        log("cfg5 paged ...")
+        ms, nb = bench_paged(L, _lib, torch, iters)
+        sec["paged_gbs"] = nb / (ms * 1e-3) / 1e9
+        sec["paged_ms"] = ms
+
+    line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic N(0,1) (torch CUDA generator, seed 0)"}
+    if c3 is not None:
+        step_ms = c3["wall_ms"]
+        line.update({
+            "value": round(3.5 * c3["F"] / (step_ms * 1e-3) / 1e12, 2),
+            "unit": "TFLOP/s",
+            "ms_per_step": round(step_ms, 4),
+            "config": {"workload": "config 3: flash_attention fwd+bwd, bf16, causal GQA, B=2 Hq=16 "
+                                   "Hkv=4 S=8192 D=128 (dK/dV group-summed, LSE saved)",
+                       "batch": 2, "seq_len": 8192, "head_dim": 128, "num_heads": 16,
+                       "num_kv_heads": 4, "causal": True},
+        })
+        dom = max(c3["credit"], key=lambda k: c3["kern_ms"][k])
+        achieved = c3["credit"][dom] / (c3["kern_ms"][dom] * 1e-3) / 1e12
+        line["roofline"] = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+                            "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                            "traffic": load_traffic(dom, "cfg3"),
+                            "avg_launch_ms": round(c3["kern_ms"][dom], 4)}
+        if not args.skip_cpu:
+            log("cpu baseline ...")
+            line["cpu_baseline"] = cpu_baseline(c3)
+    line["secondary"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in sec.items()}
+    if "decode_gbs" in sec:
+        line["secondary"]["decode_frac_hbm"] = round(sec["decode_gbs"] / PEAK_HBM_GBS, 4)
+    if "paged_gbs" in sec:
+        line["secondary"]["paged_frac_hbm"] = round(sec["paged_gbs"] / PEAK_HBM_GBS, 4)
+    if "fwd_tflops" in sec:
+        line["secondary"]["fwd_frac_mfma"] = round(sec["fwd_tflops"] / PEAK_BF16_TFLOPS, 4)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,194 @@
+/*
+ * pallas_flash_amd.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * One entry point per launch site of the reference's Pallas operator layer
+ * (aabhimittal/TPU-Native-Pallas-FlashAttention, src/pallas_flash). Each entry
+ * point takes a plain-old-data argument struct (device pointers, sizes,
+ * scalars) plus a HIP stream passed as `void*` (a hipStream_t; NULL = the
+ * default stream), and returns a pf_status. No torch, XLA or HIP types appear
+ * in the signatures.
+ *
+ * Conventions
+ *  - Layout: every tensor is dense row-major (C-contiguous) in the shape given
+ *    in the struct comments; element strides are implied by the shape.
+ *  - Ownership: the caller allocates every buffer, including workspaces.
+ *    Entry points never allocate, free or synchronise; they enqueue kernels on
+ *    `stream` and return.
+ *  - Validation happens on the host before any HIP call; a rejected call
+ *    enqueues nothing. After enqueueing, hipGetLastError() is checked and a
+ *    launch failure is reported as PF_ERR_LAUNCH.
+ *  - Thread safety: stateless and reentrant.
+ *  - Data types: dtype tags PF_DTYPE_F32 / PF_DTYPE_BF16 / PF_DTYPE_F16 name
+ *    the storage type of q/k/v/o (and do/dq/dk/dv); all arithmetic is float32
+ *    (MFMA with float32 accumulation). LSE / delta are always float32.
+ *  - head_dim must be 64 or 128.
+ */
+#ifndef PALLAS_FLASH_AMD_H
+#define PALLAS_FLASH_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  PF_OK = 0,
+  PF_ERR_INVALID = -1,      /* bad shape / pointer / scalar argument      */
+  PF_ERR_UNSUPPORTED = -2,  /* valid but not implemented (dtype, head_dim) */
+  PF_ERR_WORKSPACE = -3,    /* workspace missing or too small             */
+  PF_ERR_LAUNCH = -4        /* HIP reported an error at launch            */
+} pf_status;
+
+typedef enum { PF_DTYPE_F32 = 0, PF_DTYPE_BF16 = 1, PF_DTYPE_F16 = 2 } pf_dtype;
+
+/* ---------------------------------------------------------------------------
+ * Forward prefill: o = softmax(scale * q k^T + mask) v, plus LSE.
+ * Replaces the `flash_attention_fwd` pallas_call
+ * (flash_attention.py:162-227, kernel :61-159).
+ *   q   [batch, num_heads,    seq_len_q, head_dim]
+ *   k,v [batch, num_kv_heads, seq_len_k, head_dim]
+ *   o   [batch, num_heads,    seq_len_q, head_dim]   (same dtype as q)
+ *   lse [batch, num_heads,    seq_len_q] float32, natural log of the scaled
+ *       scores; may be NULL (not written). Rows with no valid key get o = 0,
+ *       lse = 0.
+ *   kv_len in (0, seq_len_k]; keys >= kv_len are never read.
+ *   causal: q_pos >= k_pos, top-left aligned (also when seq_len_q != seq_len_k).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int32_t batch, num_heads, num_kv_heads, seq_len_q, seq_len_k, head_dim;
+  int32_t kv_len;
+  int32_t causal;
+  float sm_scale;
+  int32_t dtype;
+} pf_attn_fwd_args;
+
+int pf_attn_fwd(const pf_attn_fwd_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused-RoPE forward (no LSE). Replaces the `flash_attention_rope_fwd`
+ * pallas_call (fused_rope.py:183-213, kernel :53-113). Q and K are rotated in
+ * float32 (x*cos + rotate_half(x)*sin) while their tiles are staged.
+ *   q_cos, q_sin [seq_len_q, head_dim] float32
+ *   k_cos, k_sin [seq_len_k, head_dim] float32
+ * Other fields as pf_attn_fwd_args (lse is ignored and may be NULL).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  pf_attn_fwd_args base;
+  const float* q_cos;
+  const float* q_sin;
+  const float* k_cos;
+  const float* k_sin;
+} pf_attn_fwd_rope_args;
+
+int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Backward. Replaces `_flash_attention_bwd_call` (flash_attention.py:354-442):
+ * the delta preprocess (:363-365), the `flash_attention_bwd_dq` pallas_call
+ * (:379-398) and the `flash_attention_bwd_dkv` pallas_call plus the GQA group
+ * sum (:403-436).
+ *   q, o, do_, dq [batch, num_heads,    seq_len_q, head_dim]  (dtype)
+ *   k, v, dk, dv  [batch, num_kv_heads, seq_len_k, head_dim]  (dtype)
+ *   lse           [batch, num_heads, seq_len_q] float32 (from pf_attn_fwd)
+ *   delta         [batch, num_heads, seq_len_q] float32 workspace; written by
+ *                 pf_attn_bwd_delta, read by the dq / dkv kernels.
+ * dk/dv are summed over the num_heads/num_kv_heads query heads of each group in
+ * float32 before the single cast to dtype. Keys >= kv_len get zero gradient.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* do_;
+  const float* lse;
+  float* delta;
+  void* dq;
+  void* dk;
+  void* dv;
+  int32_t batch, num_heads, num_kv_heads, seq_len_q, seq_len_k, head_dim;
+  int32_t kv_len;
+  int32_t causal;
+  float sm_scale;
+  int32_t dtype;
+} pf_attn_bwd_args;
+
+int pf_attn_bwd_delta(const pf_attn_bwd_args* args, void* stream);
+int pf_attn_bwd_dq(const pf_attn_bwd_args* args, void* stream);
+int pf_attn_bwd_dkv(const pf_attn_bwd_args* args, void* stream);
+/* delta, then dq and dkv, on one stream */
+int pf_attn_bwd(const pf_attn_bwd_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Single-query decode against a contiguous KV cache. Replaces
+ * `flash_attention_decode` (flash_attention.py:555-589), which the reference
+ * runs as the forward pallas_call with block_q = 1 and kv_len = cache_len.
+ * Split-KV: partial (m, l, acc) per KV chunk into `workspace`, then a combine.
+ *   q [batch, num_heads, 1, head_dim]; o same shape
+ *   k_cache, v_cache [batch, num_kv_heads, cache_size, head_dim]
+ *   cache_len in (0, cache_size]; slots >= cache_len are never read.
+ * workspace: at least pf_attn_decode_workspace_size(args) bytes, 256-byte
+ * aligned device memory (contents on entry do not matter).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  void* o;
+  int32_t batch, num_heads, num_kv_heads, cache_size, head_dim;
+  int32_t cache_len;
+  float sm_scale;
+  int32_t dtype;
+  void* workspace;
+  size_t workspace_bytes;
+} pf_attn_decode_args;
+
+size_t pf_attn_decode_workspace_size(const pf_attn_decode_args* args);
+int pf_attn_decode(const pf_attn_decode_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged single-query attention. Replaces the `paged_flash_attention`
+ * pallas_call (paged.py:151-192, kernel :45-99).
+ *   q [batch, num_heads, 1, head_dim]; o same shape
+ *   k_pages, v_pages [num_pages, num_kv_heads, page_size, head_dim]
+ *   block_tables [batch, pages_per_seq] int32 (device): logical -> physical
+ *   context_lens [batch] int32 (device): valid tokens per sequence.
+ * Sequence b attends min(context_lens[b], pages_per_seq*page_size) tokens; a
+ * non-positive length gives o = 0. Table entries at logical pages at or past
+ * ceil(len / page_size) are never read (so -1 padding is legal); live entries
+ * are clamped into [0, num_pages). page_size must be a multiple of 16.
+ * workspace: at least pf_paged_attn_workspace_size(args) bytes.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* q;
+  const void* k_pages;
+  const void* v_pages;
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  void* o;
+  int32_t batch, num_heads, num_kv_heads, num_pages, page_size, head_dim;
+  int32_t pages_per_seq;
+  float sm_scale;
+  int32_t dtype;
+  void* workspace;
+  size_t workspace_bytes;
+} pf_paged_attn_args;
+
+size_t pf_paged_attn_workspace_size(const pf_paged_attn_args* args);
+int pf_paged_attn(const pf_paged_attn_args* args, void* stream);
+
+/* Library version string (static storage). */
+const char* pf_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PALLAS_FLASH_AMD_H */

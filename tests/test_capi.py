@@ -1,0 +1,145 @@
+"""CPU tier: the C-ABI library loads, exports every symbol the header declares,
+and rejects invalid arguments on the host before touching a device.
+
+No call here reaches a kernel launch: every call carries an argument the host
+validation refuses (or is a pure-host query such as the workspace size).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+from pallas_flash import _lib
+
+HEADER = os.path.join(ROOT, "include", "pallas_flash_amd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(pf_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.lib()
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared_functions()
+    for want in ("pf_attn_fwd", "pf_attn_fwd_rope", "pf_attn_bwd", "pf_attn_bwd_delta",
+                 "pf_attn_bwd_dq", "pf_attn_bwd_dkv", "pf_attn_decode",
+                 "pf_attn_decode_workspace_size", "pf_paged_attn", "pf_paged_attn_workspace_size",
+                 "pf_version"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(L):
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature in _lib.py"
+
+
+def test_version(L):
+    assert b"gfx950" in L.pf_version()
+
+
+def test_struct_sizes_match_c_layout():
+    # pointers 8 bytes; int32/float 4; size_t 8 (x86-64 SysV)
+    assert ctypes.sizeof(_lib.FwdArgs) == 5 * 8 + 10 * 4
+    assert ctypes.sizeof(_lib.FwdRopeArgs) == ctypes.sizeof(_lib.FwdArgs) + 4 * 8
+    assert ctypes.sizeof(_lib.BwdArgs) == 10 * 8 + 10 * 4
+    assert ctypes.sizeof(_lib.DecodeArgs) == 4 * 8 + 8 * 4 + 8 + 8
+    assert ctypes.sizeof(_lib.PagedArgs) == 6 * 8 + 9 * 4 + 4 + 8 + 8
+
+
+def _fwd(**over):
+    base = dict(q=8, k=8, v=8, o=8, lse=None, batch=1, num_heads=4, num_kv_heads=2, seq_len_q=16,
+                seq_len_k=16, head_dim=128, kv_len=16, causal=0, sm_scale=0.1, dtype=1)
+    base.update(over)
+    return _lib.FwdArgs(**base)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(num_heads=6, num_kv_heads=4), _lib.PF_ERR_INVALID),        # flash_attention.py:537
+    (dict(kv_len=0), _lib.PF_ERR_INVALID),                           # :544
+    (dict(kv_len=17), _lib.PF_ERR_INVALID),
+    (dict(num_kv_heads=0), _lib.PF_ERR_INVALID),
+    (dict(q=None), _lib.PF_ERR_INVALID),
+    (dict(sm_scale=float("nan")), _lib.PF_ERR_INVALID),
+    (dict(head_dim=96), _lib.PF_ERR_UNSUPPORTED),
+    (dict(dtype=7), _lib.PF_ERR_UNSUPPORTED),
+])
+def test_fwd_rejects_on_host(L, over, status):
+    assert L.pf_attn_fwd(_fwd(**over), None) == status
+
+
+def test_fwd_null_args(L):
+    assert L.pf_attn_fwd(None, None) == _lib.PF_ERR_INVALID
+
+
+def test_rope_requires_tables(L):
+    args = _lib.FwdRopeArgs(_fwd(), None, None, None, None)
+    assert L.pf_attn_fwd_rope(args, None) == _lib.PF_ERR_INVALID
+
+
+def test_bwd_requires_buffers(L):
+    a = _lib.BwdArgs(q=8, k=8, v=8, o=8, do_=8, lse=8, delta=8, dq=8, dk=8, dv=None, batch=1,
+                     num_heads=2, num_kv_heads=2, seq_len_q=8, seq_len_k=8, head_dim=128, kv_len=8,
+                     causal=1, sm_scale=0.1, dtype=0)
+    for fn in (L.pf_attn_bwd, L.pf_attn_bwd_dkv, L.pf_attn_bwd_dq):
+        assert fn(a, None) == _lib.PF_ERR_INVALID
+    a.dv = 8
+    a.num_heads = 3
+    assert L.pf_attn_bwd(a, None) == _lib.PF_ERR_INVALID
+
+
+def _dec(**over):
+    base = dict(q=8, k_cache=8, v_cache=8, o=8, batch=64, num_heads=32, num_kv_heads=8,
+                cache_size=8192, head_dim=128, cache_len=6000, sm_scale=0.1, dtype=1,
+                workspace=None, workspace_bytes=0)
+    base.update(over)
+    return _lib.DecodeArgs(**base)
+
+
+def test_decode_workspace_and_rejections(L):
+    ws = L.pf_attn_decode_workspace_size(_dec())
+    assert ws > 0 and ws % 256 == 0
+    # workspace missing -> rejected before launch
+    assert L.pf_attn_decode(_dec(), None) == _lib.PF_ERR_WORKSPACE
+    assert L.pf_attn_decode(_dec(workspace=256, workspace_bytes=ws - 1), None) == _lib.PF_ERR_WORKSPACE
+    assert L.pf_attn_decode(_dec(workspace=100, workspace_bytes=ws), None) == _lib.PF_ERR_WORKSPACE
+    assert L.pf_attn_decode(_dec(cache_len=0), None) == _lib.PF_ERR_INVALID
+    assert L.pf_attn_decode(_dec(cache_len=8193), None) == _lib.PF_ERR_INVALID
+    assert L.pf_attn_decode_workspace_size(_dec(num_heads=30)) == 0
+
+
+def _paged(**over):
+    base = dict(q=8, k_pages=8, v_pages=8, block_tables=8, context_lens=8, o=8, batch=128,
+                num_heads=32, num_kv_heads=8, num_pages=16384, page_size=64, head_dim=128,
+                pages_per_seq=128, sm_scale=0.1, dtype=1, workspace=None, workspace_bytes=0)
+    base.update(over)
+    return _lib.PagedArgs(**base)
+
+
+def test_paged_workspace_and_rejections(L):
+    ws = L.pf_paged_attn_workspace_size(_paged())
+    assert ws > 0
+    assert L.pf_paged_attn(_paged(), None) == _lib.PF_ERR_WORKSPACE
+    assert L.pf_paged_attn(_paged(num_heads=12), None) == _lib.PF_ERR_INVALID
+    assert L.pf_paged_attn(_paged(context_lens=None, workspace=256, workspace_bytes=ws), None) == _lib.PF_ERR_INVALID
+    assert L.pf_paged_attn(_paged(head_dim=80), None) == _lib.PF_ERR_UNSUPPORTED
+
+
+def test_status_mapping():
+    _lib.check(_lib.PF_OK, "x")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.PF_ERR_INVALID, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.PF_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.PF_ERR_LAUNCH, "x")

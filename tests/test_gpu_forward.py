@@ -1,0 +1,147 @@
+"""GPU tier: forward prefill kernel vs the float64 oracle.
+
+Re-expresses the reference's test_flash_attention.py (shapes :24-30, GQA
+:44-54, block sizes :64-70, custom scale :73-78) and test_bfloat16.py
+(:18-47) against this build's oracle, with the north-star tolerances, plus
+cases the reference leaves implicit (kv_len with a NaN tail, Sq != Sk, LSE,
+head_dim 64, float16).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import check_fwd, dev, host, max_abs, note, qkv, rel_err
+from oracle import attention_ref
+from pallas_flash import flash_attention, flash_attention_with_lse
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1, 128), (1, 2, 256), (2, 3, 384), (1, 2, 200), (1, 2, 130)]
+
+
+def _run(dt, B, Hq, Hkv, Sq, Sk, causal, seed=0, D=128, kv_len=None, sm_scale=None, **kw):
+    note(f"fwd dt={dt} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Sk={Sk} D={D} causal={causal} kv_len={kv_len}")
+    rng = np.random.default_rng(seed)
+    q, k, v = qkv(rng, B, Hq, Hkv, Sq, Sk, D)
+    tq, tk, tv = dev(q, dt), dev(k, dt), dev(v, dt)
+    out = flash_attention(tq, tk, tv, causal=causal, kv_len=kv_len, sm_scale=sm_scale, **kw)
+    torch.cuda.synchronize()
+    assert out.shape == tq.shape and out.dtype == tq.dtype
+    ref, _ = attention_ref(host(tq), host(tk), host(tv), causal=causal, kv_len=kv_len,
+                           sm_scale=sm_scale)
+    return host(out), ref, (q, k, v)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_matches_reference_f32(shape, causal):
+    B, H, S = shape
+    out, ref, _ = _run("f32", B, H, H, S, S, causal)
+    check_fwd(out, ref, "f32")
+    assert max_abs(out, ref) < 2e-3  # the reference's own bound
+
+
+@pytest.mark.parametrize("n_heads,n_kv_heads", [(8, 2), (8, 1), (4, 4)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_grouped_query_attention(n_heads, n_kv_heads, causal):
+    out, ref, _ = _run("f32", 1, n_heads, n_kv_heads, 256, 256, causal, seed=7)
+    check_fwd(out, ref, "f32")
+
+
+@pytest.mark.parametrize("block", [(64, 64), (128, 256), (256, 128)])
+def test_block_size_hints_accepted(block):
+    out, ref, _ = _run("f32", 1, 2, 2, 512, 512, True, seed=1, block_q=block[0], block_k=block[1])
+    check_fwd(out, ref, "f32")
+
+
+def test_custom_scale():
+    out, ref, _ = _run("f32", 1, 2, 2, 256, 256, False, seed=2, sm_scale=0.05)
+    check_fwd(out, ref, "f32")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("n_heads,n_kv_heads", [(2, 2), (4, 2)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_half_forward(dt, n_heads, n_kv_heads, causal):
+    out, ref, (q, k, v) = _run(dt, 1, n_heads, n_kv_heads, 256, 256, causal)
+    check_fwd(out, ref, dt)
+    # test_bfloat16.py:29-38: against the f32 oracle on the *unrounded* inputs
+    ref_unrounded, _ = attention_ref(q, k, v, causal=causal)
+    assert max_abs(out, ref_unrounded) < 3e-2
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Sq,Sk", [(100, 300), (300, 100), (1, 200), (129, 129)])
+def test_ragged_and_unequal_lengths(dt, causal, Sq, Sk):
+    out, ref, _ = _run(dt, 2, 4, 2, Sq, Sk, causal, seed=3)
+    check_fwd(out, ref, dt)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_kv_len_with_nan_tail(dt, causal):
+    rng = np.random.default_rng(4)
+    q, k, v = qkv(rng, 1, 4, 2, 200, 320)
+    kv_len = 157
+    k[:, :, kv_len:] = np.nan
+    v[:, :, kv_len:] = np.nan
+    note(f"fwd nan-tail dt={dt} causal={causal}")
+    tq, tk, tv = dev(q, dt), dev(k, dt), dev(v, dt)
+    out = host(flash_attention(tq, tk, tv, causal=causal, kv_len=kv_len))
+    ref, _ = attention_ref(host(tq), host(tk), host(tv), causal=causal, kv_len=kv_len)
+    check_fwd(out, ref, dt)
+    # bitwise: the tail's content cannot matter
+    k2, v2 = k.copy(), v.copy()
+    k2[:, :, kv_len:] = 7.0
+    v2[:, :, kv_len:] = -3.0
+    out2 = host(flash_attention(tq, dev(k2, dt), dev(v2, dt), causal=causal, kv_len=kv_len))
+    np.testing.assert_array_equal(out, out2)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_lse(dt, causal):
+    rng = np.random.default_rng(5)
+    q, k, v = qkv(rng, 2, 4, 1, 190, 190)
+    tq, tk, tv = dev(q, dt), dev(k, dt), dev(v, dt)
+    note(f"fwd lse dt={dt} causal={causal}")
+    out, lse = flash_attention_with_lse(tq, tk, tv, causal=causal, kv_len=170)
+    ro, rl = attention_ref(host(tq), host(tk), host(tv), causal=causal, kv_len=170)
+    check_fwd(host(out), ro, dt)
+    assert lse.dtype == torch.float32 and lse.shape == (2, 4, 190)
+    assert max_abs(host(lse), rl) < (1e-5 if dt == "f32" else 1e-3)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_dim_64(dt, causal):
+    out, ref, _ = _run(dt, 1, 4, 2, 200, 200, causal, D=64, seed=6)
+    check_fwd(out, ref, dt)
+
+
+def test_closed_forms_on_device():
+    # one valid key -> v0 exactly (up to rounding of 1.0 * v0)
+    rng = np.random.default_rng(8)
+    q, k, v = qkv(rng, 1, 2, 1, 64, 64)
+    note("fwd closed forms")
+    out = host(flash_attention(dev(q, "f32"), dev(k, "f32"), dev(v, "f32"), kv_len=1))
+    np.testing.assert_allclose(out, np.broadcast_to(v[0, 0, 0], out.shape), rtol=1e-6)
+    # causal row 0 -> v[0]
+    out = host(flash_attention(dev(q, "f32"), dev(k, "f32"), dev(v, "f32"), causal=True))
+    np.testing.assert_allclose(out[0, :, 0], np.broadcast_to(v[0, 0, 0], (2, 128)), rtol=1e-6)
+
+
+def test_nondefault_stream_and_device_guard():
+    rng = np.random.default_rng(9)
+    q, k, v = qkv(rng, 1, 2, 2, 64, 64)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        tq, tk, tv = dev(q, "f32"), dev(k, "f32"), dev(v, "f32")
+        out = flash_attention(tq, tk, tv, causal=True)
+    s.synchronize()
+    ref, _ = attention_ref(host(tq), host(tk), host(tv), causal=True)
+    assert rel_err(host(out), ref) < 1e-5

@@ -1,0 +1,297 @@
+// extern "C" entry points of libpallas_flash_amd.so (declared in
+// include/pallas_flash_amd.h). Each one validates its arguments on the host
+// (no HIP call before validation passes), fills a kernel parameter block and
+// enqueues on the caller's stream. Nothing here allocates or synchronises.
+#include <math.h>
+
+#include "../../include/pallas_flash_amd.h"
+#include "pf_kernels.hpp"
+
+namespace {
+
+bool dtype_ok(int32_t d) { return d == PF_DTYPE_F32 || d == PF_DTYPE_BF16 || d == PF_DTYPE_F16; }
+bool head_dim_ok(int32_t d) { return d == 64 || d == 128; }
+
+constexpr int64_t kMaxGrid = 0x7fffffff;
+
+int check_attn_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int32_t D,
+                    int32_t kv_len, float scale, int32_t dtype) {
+  // flash_attention.py:527-545: ranks/shape agreement, Hq % Hkv, kv_len in (0, Sk].
+  if (B < 0 || Hq < 1 || Hkv < 1 || Sq < 0 || Sk < 1 || D < 1) return PF_ERR_INVALID;
+  if (Hq % Hkv != 0) return PF_ERR_INVALID;
+  if (kv_len < 1 || kv_len > Sk) return PF_ERR_INVALID;
+  if (!isfinite(scale)) return PF_ERR_INVALID;
+  if (!dtype_ok(dtype)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(D)) return PF_ERR_UNSUPPORTED;
+  return PF_OK;
+}
+
+int finish(hipError_t e) { return e == hipSuccess ? PF_OK : PF_ERR_LAUNCH; }
+
+int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
+  int st = check_attn_dims(a->batch, a->num_heads, a->num_kv_heads, a->seq_len_q, a->seq_len_k,
+                           a->head_dim, a->kv_len, a->sm_scale, a->dtype);
+  if (st != PF_OK) return st;
+  if (!a->q || !a->k || !a->v || !a->o) return PF_ERR_INVALID;
+  p->q = a->q;
+  p->k = a->k;
+  p->v = a->v;
+  p->o = a->o;
+  p->lse = a->lse;
+  p->q_cos = p->q_sin = p->k_cos = p->k_sin = nullptr;
+  p->B = a->batch;
+  p->Hq = a->num_heads;
+  p->Hkv = a->num_kv_heads;
+  p->Sq = a->seq_len_q;
+  p->Sk = a->seq_len_k;
+  p->kv_len = a->kv_len;
+  p->g = a->num_heads / a->num_kv_heads;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p->n_qblk = (a->seq_len_q + 127) / 128;
+  const int64_t n_work = (int64_t)a->batch * a->num_heads * p->n_qblk;
+  if (n_work > kMaxGrid) return PF_ERR_UNSUPPORTED;
+  p->n_work = (int)n_work;
+  return PF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pf_version(void) { return "pallas_flash_amd 0.1.0 (gfx950)"; }
+
+int pf_attn_fwd(const pf_attn_fwd_args* a, void* stream) {
+  if (!a) return PF_ERR_INVALID;
+  pf::FwdParams p;
+  int st = fill_fwd(a, &p);
+  if (st != PF_OK) return st;
+  if (p.n_work == 0) return PF_OK;
+  return finish(pf::launch_attn_fwd(p, a->dtype, a->head_dim, a->causal != 0, false,
+                                    (hipStream_t)stream));
+}
+
+int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* a, void* stream) {
+  if (!a) return PF_ERR_INVALID;
+  pf::FwdParams p;
+  int st = fill_fwd(&a->base, &p);
+  if (st != PF_OK) return st;
+  if (!a->q_cos || !a->q_sin || !a->k_cos || !a->k_sin) return PF_ERR_INVALID;
+  if (a->base.head_dim % 2 != 0) return PF_ERR_INVALID;  // fused_rope.py:168-169
+  p.q_cos = a->q_cos;
+  p.q_sin = a->q_sin;
+  p.k_cos = a->k_cos;
+  p.k_sin = a->k_sin;
+  p.lse = nullptr;  // the reference's fused kernel has no LSE output
+  if (p.n_work == 0) return PF_OK;
+  return finish(pf::launch_attn_fwd(p, a->base.dtype, a->base.head_dim, a->base.causal != 0, true,
+                                    (hipStream_t)stream));
+}
+
+// ---------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------
+static int fill_bwd(const pf_attn_bwd_args* a, pf::BwdParams* p, bool need_grads) {
+  if (!a) return PF_ERR_INVALID;
+  int st = check_attn_dims(a->batch, a->num_heads, a->num_kv_heads, a->seq_len_q, a->seq_len_k,
+                           a->head_dim, a->kv_len, a->sm_scale, a->dtype);
+  if (st != PF_OK) return st;
+  if (!a->o || !a->do_ || !a->delta) return PF_ERR_INVALID;
+  if (need_grads && (!a->q || !a->k || !a->v || !a->lse || !a->dq || !a->dk || !a->dv))
+    return PF_ERR_INVALID;
+  p->q = a->q;
+  p->k = a->k;
+  p->v = a->v;
+  p->o = a->o;
+  p->dout = a->do_;
+  p->lse = a->lse;
+  p->delta = a->delta;
+  p->dq = a->dq;
+  p->dk = a->dk;
+  p->dv = a->dv;
+  p->B = a->batch;
+  p->Hq = a->num_heads;
+  p->Hkv = a->num_kv_heads;
+  p->Sq = a->seq_len_q;
+  p->Sk = a->seq_len_k;
+  p->kv_len = a->kv_len;
+  p->g = a->num_heads / a->num_kv_heads;
+  p->sm_scale = a->sm_scale;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  const int64_t rows = (int64_t)a->batch * a->num_heads * a->seq_len_q;
+  if (rows > kMaxGrid) return PF_ERR_UNSUPPORTED;
+  return PF_OK;
+}
+
+int pf_attn_bwd_delta(const pf_attn_bwd_args* a, void* stream) {
+  pf::BwdParams p;
+  int st = fill_bwd(a, &p, false);
+  if (st != PF_OK) return st;
+  if ((int64_t)p.B * p.Hq * p.Sq == 0) return PF_OK;
+  return finish(pf::launch_attn_bwd_delta(p, a->dtype, a->head_dim, (hipStream_t)stream));
+}
+
+int pf_attn_bwd_dq(const pf_attn_bwd_args* a, void* stream) {
+  pf::BwdParams p;
+  int st = fill_bwd(a, &p, true);
+  if (st != PF_OK) return st;
+  if ((int64_t)p.B * p.Hq * p.Sq == 0) return PF_OK;
+  return finish(pf::launch_attn_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, (hipStream_t)stream));
+}
+
+int pf_attn_bwd_dkv(const pf_attn_bwd_args* a, void* stream) {
+  pf::BwdParams p;
+  int st = fill_bwd(a, &p, true);
+  if (st != PF_OK) return st;
+  if ((int64_t)p.B * p.Hkv * p.Sk == 0) return PF_OK;
+  return finish(pf::launch_attn_bwd_dkv(p, a->dtype, a->head_dim, a->causal != 0, (hipStream_t)stream));
+}
+
+int pf_attn_bwd(const pf_attn_bwd_args* a, void* stream) {
+  pf::BwdParams p;
+  int st = fill_bwd(a, &p, true);
+  if (st != PF_OK) return st;
+  hipStream_t s = (hipStream_t)stream;
+  if ((int64_t)p.B * p.Hq * p.Sq > 0) {
+    st = finish(pf::launch_attn_bwd_delta(p, a->dtype, a->head_dim, s));
+    if (st != PF_OK) return st;
+    st = finish(pf::launch_attn_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, s));
+    if (st != PF_OK) return st;
+  }
+  if ((int64_t)p.B * p.Hkv * p.Sk > 0)
+    st = finish(pf::launch_attn_bwd_dkv(p, a->dtype, a->head_dim, a->causal != 0, s));
+  return st;
+}
+
+// ---------------------------------------------------------------------------
+// Decode (contiguous cache) and paged decode
+// ---------------------------------------------------------------------------
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Key-chunk size for split-KV: enough (b, kv head, chunk) waves to fill the
+// chip several times over (256 CUs x 8 resident waves), chunks a multiple of
+// the 64-key block and at least 256 keys so each wave streams a useful run.
+static int decode_chunk(int64_t units, int max_len) {
+  const int64_t target_waves = 4096;
+  int64_t n_split = (target_waves + units - 1) / (units > 0 ? units : 1);
+  if (n_split < 1) n_split = 1;
+  int64_t chunk = (max_len + n_split - 1) / n_split;
+  chunk = ((chunk + 63) / 64) * 64;
+  if (chunk < 256) chunk = 256;
+  return (int)chunk;
+}
+
+static int fill_decode(const pf_attn_decode_args* a, pf::DecodeParams* p) {
+  if (!a) return PF_ERR_INVALID;
+  if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->cache_size < 1)
+    return PF_ERR_INVALID;
+  if (a->num_heads % a->num_kv_heads != 0) return PF_ERR_INVALID;
+  if (a->cache_len < 1 || a->cache_len > a->cache_size) return PF_ERR_INVALID;
+  if (!isfinite(a->sm_scale)) return PF_ERR_INVALID;
+  if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  const int g = a->num_heads / a->num_kv_heads;
+  const int64_t units = (int64_t)a->batch * a->num_kv_heads * ((g + 31) / 32);
+  *p = pf::DecodeParams{};
+  p->q = a->q;
+  p->k = a->k_cache;
+  p->v = a->v_cache;
+  p->o = a->o;
+  p->B = a->batch;
+  p->Hq = a->num_heads;
+  p->Hkv = a->num_kv_heads;
+  p->D = a->head_dim;
+  p->cache_size = a->cache_size;
+  p->cache_len = a->cache_len;
+  p->chunk = decode_chunk(units, a->cache_len);
+  p->n_split = (a->cache_len + p->chunk - 1) / p->chunk;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  if (units * p->n_split > kMaxGrid) return PF_ERR_UNSUPPORTED;
+  return PF_OK;
+}
+
+static size_t decode_ws_bytes(const pf::DecodeParams& p) {
+  const size_t slots = (size_t)p.B * p.Hq * p.n_split;
+  return align256(slots * p.D * sizeof(float)) + align256(slots * 2 * sizeof(float));
+}
+
+static int bind_workspace(pf::DecodeParams* p, void* ws, size_t bytes) {
+  const size_t need = decode_ws_bytes(*p);
+  if (need == 0) return PF_OK;
+  if (!ws || bytes < need || ((uintptr_t)ws & 255) != 0) return PF_ERR_WORKSPACE;
+  const size_t slots = (size_t)p->B * p->Hq * p->n_split;
+  p->part_o = static_cast<float*>(ws);
+  p->part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(slots * p->D * sizeof(float)));
+  return PF_OK;
+}
+
+size_t pf_attn_decode_workspace_size(const pf_attn_decode_args* a) {
+  pf::DecodeParams p;
+  if (fill_decode(a, &p) != PF_OK) return 0;
+  return decode_ws_bytes(p);
+}
+
+int pf_attn_decode(const pf_attn_decode_args* a, void* stream) {
+  pf::DecodeParams p;
+  int st = fill_decode(a, &p);
+  if (st != PF_OK) return st;
+  if (!a->q || !a->k_cache || !a->v_cache || !a->o) return PF_ERR_INVALID;
+  if (a->batch == 0) return PF_OK;
+  st = bind_workspace(&p, a->workspace, a->workspace_bytes);
+  if (st != PF_OK) return st;
+  return finish(pf::launch_decode(p, a->dtype, false, (hipStream_t)stream));
+}
+
+static int fill_paged(const pf_paged_attn_args* a, pf::DecodeParams* p) {
+  if (!a) return PF_ERR_INVALID;
+  // paged.py:129-149: Sq == 1 (implied by the struct), heads divisible, table [B, P], lens [B].
+  if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->num_pages < 1 ||
+      a->page_size < 1 || a->pages_per_seq < 0)
+    return PF_ERR_INVALID;
+  if (a->num_heads % a->num_kv_heads != 0) return PF_ERR_INVALID;
+  if (!isfinite(a->sm_scale)) return PF_ERR_INVALID;
+  if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  const int64_t max_len = (int64_t)a->pages_per_seq * a->page_size;
+  if (max_len > 0x7fffffff) return PF_ERR_UNSUPPORTED;
+  const int g = a->num_heads / a->num_kv_heads;
+  const int64_t units = (int64_t)a->batch * a->num_kv_heads * ((g + 31) / 32);
+  *p = pf::DecodeParams{};
+  p->q = a->q;
+  p->k = a->k_pages;
+  p->v = a->v_pages;
+  p->o = a->o;
+  p->block_tables = a->block_tables;
+  p->context_lens = a->context_lens;
+  p->B = a->batch;
+  p->Hq = a->num_heads;
+  p->Hkv = a->num_kv_heads;
+  p->D = a->head_dim;
+  p->num_pages = a->num_pages;
+  p->page_size = a->page_size;
+  p->pages_per_seq = a->pages_per_seq;
+  p->chunk = decode_chunk(units, (int)(max_len > 0 ? max_len : 1));
+  p->n_split = max_len > 0 ? (int)((max_len + p->chunk - 1) / p->chunk) : 1;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  if (units * p->n_split > kMaxGrid) return PF_ERR_UNSUPPORTED;
+  return PF_OK;
+}
+
+size_t pf_paged_attn_workspace_size(const pf_paged_attn_args* a) {
+  pf::DecodeParams p;
+  if (fill_paged(a, &p) != PF_OK) return 0;
+  return decode_ws_bytes(p);
+}
+
+int pf_paged_attn(const pf_paged_attn_args* a, void* stream) {
+  pf::DecodeParams p;
+  int st = fill_paged(a, &p);
+  if (st != PF_OK) return st;
+  if (!a->q || !a->k_pages || !a->v_pages || !a->o || !a->context_lens) return PF_ERR_INVALID;
+  if (a->pages_per_seq > 0 && !a->block_tables) return PF_ERR_INVALID;
+  if (a->batch == 0) return PF_OK;
+  st = bind_workspace(&p, a->workspace, a->workspace_bytes);
+  if (st != PF_OK) return st;
+  return finish(pf::launch_decode(p, a->dtype, true, (hipStream_t)stream));
+}
+
+}  // extern "C"

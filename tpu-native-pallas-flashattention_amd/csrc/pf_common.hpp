@@ -1,0 +1,165 @@
+// Shared device-side definitions for the gfx950 attention kernels.
+//
+// Element types: float (F32), __bf16 (BF16), _Float16 (F16). Every kernel
+// upcasts to float32 and accumulates in float32 (the reference's arithmetic,
+// flash_attention.py:91-93), feeding the MFMA matrix cores with the storage
+// type (bf16/f16 operands, or float32 operands for F32 inputs).
+//
+// MFMA lane layouts used throughout (verified on gfx950 with an in-bounds
+// probe: every output element of a random integer product matched):
+//   v_mfma_f32_32x32x16_{bf16,f16}: A[32 x 16]: lane l holds A[l%32][8(l/32)+t],
+//     t = 0..7; B[16 x 32]: lane l holds B[8(l/32)+t][l%32];
+//     C[32 x 32]: lane l, register r holds C[8(r/4) + 4(l/32) + r%4][l%32].
+//   v_mfma_f32_32x32x2f32: A: lane l holds A[l%32][l/32]; B: B[l/32][l%32];
+//     C as above.
+// A reduction (k) index can be assigned to (step, lane half, slot) in any
+// bijective way as long as both operands agree; the kernels use that freedom
+// so each lane half owns a contiguous range of the reduction dimension.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pf {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+typedef bf16_t bf16x8 __attribute__((ext_vector_type(8)));
+typedef f16_t f16x8 __attribute__((ext_vector_type(8)));
+typedef bf16_t bf16x4 __attribute__((ext_vector_type(4)));
+typedef f16_t f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// dtype tags shared with the C ABI (pf_dtype).
+enum : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static constexpr int kPerChunk = 4;  // elements per 16-byte chunk
+  __device__ static inline float to_f32(float x) { return x; }
+  __device__ static inline float from_f32(float x) { return x; }
+};
+template <>
+struct Elem<bf16_t> {
+  static constexpr int kPerChunk = 8;
+  __device__ static inline float to_f32(bf16_t x) { return (float)x; }
+  __device__ static inline bf16_t from_f32(float x) { return (bf16_t)x; }
+};
+template <>
+struct Elem<f16_t> {
+  static constexpr int kPerChunk = 8;
+  __device__ static inline float to_f32(f16_t x) { return (float)x; }
+  __device__ static inline f16_t from_f32(float x) { return (f16_t)x; }
+};
+
+// 32x32 MFMA with float32 accumulation. kK = reduction elements one lane
+// supplies per instruction; Frag = that operand fragment.
+template <typename T>
+struct Mfma32;
+
+template <>
+struct Mfma32<bf16_t> {
+  static constexpr int kK = 8;
+  typedef bf16x8 Frag;
+  __device__ static inline f32x16 run(Frag a, Frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma32<f16_t> {
+  static constexpr int kK = 8;
+  typedef f16x8 Frag;
+  __device__ static inline f32x16 run(Frag a, Frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma32<float> {
+  static constexpr int kK = 1;
+  typedef float Frag;
+  __device__ static inline f32x16 run(Frag a, Frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+// Number of MFMA operand fragments held in one 16-byte chunk.
+template <typename T>
+constexpr int frags_per_chunk() {
+  return 16 / (Mfma32<T>::kK * (int)sizeof(T));
+}
+
+// Reinterpret a 16-byte chunk as operand fragment i.
+template <typename T>
+__device__ inline typename Mfma32<T>::Frag chunk_frag(const u32x4& c, int i) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(float, c[i]);
+  } else {
+    return __builtin_bit_cast(typename Mfma32<T>::Frag, c);
+  }
+}
+
+// Unpack a 16-byte chunk into float32 values (kPerChunk of them).
+template <typename T>
+__device__ inline void chunk_to_f32(const u32x4& c, float* out) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(float, c[i]);
+  } else {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    v8 x = __builtin_bit_cast(v8, c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = Elem<T>::to_f32(x[i]);
+  }
+}
+
+// Pack kPerChunk float32 values into a 16-byte chunk of T (round to nearest even).
+template <typename T>
+__device__ inline u32x4 f32_to_chunk(const float* in) {
+  if constexpr (sizeof(T) == 4) {
+    u32x4 c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = __builtin_bit_cast(uint32_t, in[i]);
+    return c;
+  } else {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    v8 x;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = Elem<T>::from_f32(in[i]);
+    return __builtin_bit_cast(u32x4, x);
+  }
+}
+
+__device__ inline u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ inline void stg16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ inline u32x4 lds16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ inline void sts16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+__device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
+
+// Workgroup -> work-item remap that keeps the `group` consecutive work items
+// (the query heads of one GQA group) on one XCD. Workgroups are dispatched
+// round-robin over the 8 XCDs (XCD = blockIdx % 8); each XCD has its own L2,
+// so items sharing K/V tiles should share an XCD. Bijective on [0, n).
+__device__ inline int xcd_remap(int bid, int n, int group) {
+  const int span = 8 * group;
+  const int full = (n / span) * span;
+  if (bid >= full) return bid;
+  const int xcd = bid & 7;
+  const int slot = bid >> 3;
+  const int chunk = (slot / group) * 8 + xcd;
+  return chunk * group + (slot % group);
+}
+
+}  // namespace pf

@@ -1,0 +1,75 @@
+// Kernel parameter blocks and host-side launchers (internal to the library;
+// the public interface is include/pallas_flash_amd.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pf {
+
+// Forward prefill (optionally with fused RoPE).
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;  // may be null
+  const float* q_cos;
+  const float* q_sin;
+  const float* k_cos;
+  const float* k_sin;
+  int B, Hq, Hkv, Sq, Sk, kv_len, g;
+  float scale_log2;  // sm_scale * log2(e)
+  int n_qblk;        // ceil(Sq / 128)
+  int n_work;        // B * Hq * n_qblk
+};
+
+hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
+                           hipStream_t stream);
+
+// Backward.
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const float* lse;
+  float* delta;
+  void* dq;
+  void* dk;
+  void* dv;
+  int B, Hq, Hkv, Sq, Sk, kv_len, g;
+  float sm_scale;
+  float scale_log2;
+};
+
+hipError_t launch_attn_bwd_delta(const BwdParams& p, int dtype, int head_dim, hipStream_t stream);
+hipError_t launch_attn_bwd_dq(const BwdParams& p, int dtype, int head_dim, bool causal,
+                              hipStream_t stream);
+hipError_t launch_attn_bwd_dkv(const BwdParams& p, int dtype, int head_dim, bool causal,
+                               hipStream_t stream);
+
+// Split-KV single-query decode, contiguous cache or paged pool.
+struct DecodeParams {
+  const void* q;
+  const void* k;  // contiguous cache base, or page pool base
+  const void* v;
+  void* o;
+  const int32_t* block_tables;  // null for the contiguous cache
+  const int32_t* context_lens;  // null for the contiguous cache
+  float* part_o;                // [B, Hq, n_split, D] partial (unnormalised) outputs
+  float* part_ml;               // [B, Hq, n_split, 2] partial (max, sum)
+  int B, Hq, Hkv, D;
+  int cache_size;     // contiguous: slots per (b, kvh); paged: unused
+  int cache_len;      // contiguous: valid slots
+  int num_pages, page_size, pages_per_seq;  // paged only
+  int n_split;        // KV chunks per (b, kvh)
+  int chunk;          // keys per chunk (multiple of the page size when paged)
+  float scale_log2;
+};
+
+hipError_t launch_decode(const DecodeParams& p, int dtype, bool paged, hipStream_t stream);
+
+}  // namespace pf

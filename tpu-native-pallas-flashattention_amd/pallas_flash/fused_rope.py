@@ -1,0 +1,116 @@
+"""FlashAttention with rotary position embeddings fused into the kernel.
+
+Drop-in for the reference's ``pallas_flash.fused_rope.flash_attention_rope``
+(src/pallas_flash/fused_rope.py:116-213). Q and K are rotated in float32
+(``x * cos + rotate_half(x) * sin``) while their tiles are staged by the HIP
+kernel, so the rotated copies never touch HBM. Forward only, like the
+reference (its docstring: "for training use the differentiable
+flash_attention with RoPE applied outside").
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def _table(t: torch.Tensor, device) -> torch.Tensor:
+    # The kernel reads float32 tables; upcasting bf16/f16 tables is exact.
+    return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+class _RopeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, q_cos, q_sin, k_cos, k_sin, causal, sm_scale, kv_len):
+        B, Hq, Sq, D = q.shape
+        Hkv, Sk = k.shape[1], k.shape[2]
+        o = torch.empty_like(q)
+        if o.numel() == 0:
+            return o
+        base = _lib.FwdArgs(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), None,
+            B, Hq, Hkv, Sq, Sk, D, kv_len, int(bool(causal)), float(sm_scale), _lib.dtype_tag(q))
+        args = _lib.FwdRopeArgs(base, _lib.ptr(q_cos), _lib.ptr(q_sin), _lib.ptr(k_cos),
+                                _lib.ptr(k_sin))
+        with torch.cuda.device(q.device):
+            _lib.check(_lib.lib().pf_attn_fwd_rope(args, _lib.stream_of(q)), "flash_attention_rope")
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        raise NotImplementedError(
+            "flash_attention_rope is forward-only (as in the reference); for training apply "
+            "RoPE outside and use flash_attention")
+
+
+def flash_attention_rope(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_cos: torch.Tensor,
+    q_sin: torch.Tensor,
+    k_cos: Optional[torch.Tensor] = None,
+    k_sin: Optional[torch.Tensor] = None,
+    *,
+    causal: bool = False,
+    sm_scale: Optional[float] = None,
+    block_q: int = 128,
+    block_k: int = 128,
+    kv_len: Optional[int] = None,
+    interpret: bool = False,
+) -> torch.Tensor:
+    """Attention with RoPE applied to Q and K inside the kernel.
+
+    Equivalent to ``flash_attention(apply_rope(q), apply_rope(k), v)`` without
+    materialising the rotated Q and K.
+
+    Args:
+        q: ``[batch, num_heads, seq_len_q, head_dim]``.
+        k, v: ``[batch, num_kv_heads, seq_len_k, head_dim]``.
+        q_cos, q_sin: ``[seq_len_q, head_dim]`` tables for the query positions.
+        k_cos, k_sin: ``[seq_len_k, head_dim]``; default to the query tables
+            when ``seq_len_k == seq_len_q``.
+        causal, sm_scale, kv_len: as ``flash_attention``.
+        block_q, block_k, interpret: accepted for compatibility; ignored.
+    """
+    # fused_rope.py:154-181
+    if k_cos is None or k_sin is None:
+        if k.shape[2] != q.shape[2]:
+            raise ValueError(
+                "k_cos/k_sin are required when the key sequence length differs "
+                "from the query sequence length")
+        k_cos, k_sin = q_cos, q_sin
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be rank-4 [batch, heads, seq, head_dim] arrays")
+    batch, num_heads, seq_len_q, head_dim = q.shape
+    num_kv_heads, seq_len_k = k.shape[1], k.shape[2]
+    if k.shape != v.shape or k.shape[0] != batch or k.shape[3] != head_dim:
+        raise ValueError("k and v must share shape, and batch/head_dim with q")
+    if num_kv_heads == 0 or num_heads % num_kv_heads != 0:
+        raise ValueError(
+            f"num_heads ({num_heads}) must be a multiple of num_kv_heads ({num_kv_heads})")
+    if head_dim % 2 != 0:
+        raise ValueError(f"head_dim must be even for RoPE, got {head_dim}")
+    for name, tbl, want in (("q_cos", q_cos, seq_len_q), ("q_sin", q_sin, seq_len_q),
+                            ("k_cos", k_cos, seq_len_k), ("k_sin", k_sin, seq_len_k)):
+        if tuple(tbl.shape) != (want, head_dim):
+            raise ValueError(f"{name} must have shape {(want, head_dim)}, got {tuple(tbl.shape)}")
+    if sm_scale is None:
+        sm_scale = 1.0 / (head_dim ** 0.5)
+    if kv_len is None:
+        kv_len = seq_len_k
+    elif not 0 < kv_len <= seq_len_k:
+        raise ValueError(f"kv_len must be in (0, {seq_len_k}], got {kv_len}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    _lib.require_device(q, k, v)
+    dev = q.device
+    return _RopeFn.apply(q.contiguous(), k.contiguous(), v.contiguous(), _table(q_cos, dev),
+                         _table(q_sin, dev), _table(k_cos, dev), _table(k_sin, dev),
+                         bool(causal), float(sm_scale), int(kv_len))
+
+
+__all__ = ["flash_attention_rope"]

@@ -1,0 +1,128 @@
+"""Paged attention on MI355X: single-query attention over a page pool.
+
+Drop-in for the reference's ``pallas_flash.paged`` (src/pallas_flash/paged.py).
+Layout, as in the reference:
+
+    k_pages / v_pages : [num_pages, num_kv_heads, page_size, head_dim]
+    block_tables      : [batch, pages_per_seq]  int32  (logical -> physical page)
+    context_lens      : [batch]                 int32  (valid tokens per sequence)
+
+The HIP kernel reads the block table from device memory, so page gathering is
+address arithmetic inside the kernel. Each KV head's pages are streamed once
+for all query heads of its GQA group (the reference re-reads them per query
+head). Table entries for logical pages at or past ``ceil(len / page_size)``
+are never read, so ``-1`` padding is legal (the reference documents that its
+unused entries must be valid indices because its DMA address is formed
+regardless, paged.py:119-121).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def paged_flash_attention(
+    q: torch.Tensor,
+    k_pages: torch.Tensor,
+    v_pages: torch.Tensor,
+    block_tables,
+    context_lens,
+    *,
+    sm_scale: Optional[float] = None,
+    interpret: bool = False,
+) -> torch.Tensor:
+    """Single-query attention over a paged KV cache (reference: paged.py:102-192).
+
+    Args:
+        q: ``[batch, num_heads, 1, head_dim]``.
+        k_pages, v_pages: ``[num_pages, num_kv_heads, page_size, head_dim]``.
+        block_tables: ``[batch, pages_per_seq]`` integer table (cast to int32).
+        context_lens: ``[batch]`` valid tokens per sequence (cast to int32). A
+            sequence attends ``min(len, pages_per_seq * page_size)`` tokens;
+            a non-positive length yields zeros.
+        sm_scale: default ``1 / sqrt(head_dim)``.
+        interpret: accepted for compatibility; ignored.
+
+    Returns:
+        ``[batch, num_heads, 1, head_dim]`` in q's dtype.
+    """
+    # paged.py:129-149
+    if q.dim() != 4 or q.shape[2] != 1:
+        raise ValueError(
+            f"paged attention expects q of shape [batch, heads, 1, head_dim], got {tuple(q.shape)}")
+    if k_pages.shape != v_pages.shape:
+        raise ValueError("k_pages and v_pages must have the same shape")
+    if k_pages.dim() != 4:
+        raise ValueError("k_pages must be [num_pages, num_kv_heads, page_size, head_dim]")
+    batch, num_heads, _, head_dim = q.shape
+    num_pages, num_kv_heads, page_size, k_head_dim = k_pages.shape
+    if k_head_dim != head_dim:
+        raise ValueError("q and pages must share head_dim")
+    if num_kv_heads == 0 or num_heads % num_kv_heads != 0:
+        raise ValueError(
+            f"num_heads ({num_heads}) must be a multiple of num_kv_heads ({num_kv_heads})")
+    block_tables = torch.as_tensor(block_tables)
+    context_lens = torch.as_tensor(context_lens)
+    if block_tables.dim() != 2 or block_tables.shape[0] != batch:
+        raise ValueError(
+            f"block_tables must be [batch, pages_per_seq], got {tuple(block_tables.shape)}")
+    if tuple(context_lens.shape) != (batch,):
+        raise ValueError(f"context_lens must be [batch], got {tuple(context_lens.shape)}")
+    if q.dtype != k_pages.dtype or q.dtype != v_pages.dtype:
+        raise ValueError("q and the page pools must share a dtype")
+    if sm_scale is None:
+        sm_scale = 1.0 / (head_dim ** 0.5)
+    _lib.require_device(q, k_pages, v_pages)
+    dev = q.device
+    tables = block_tables.to(device=dev, dtype=torch.int32).contiguous()
+    lens = context_lens.to(device=dev, dtype=torch.int32).contiguous()
+    q, k_pages, v_pages = q.contiguous(), k_pages.contiguous(), v_pages.contiguous()
+    o = torch.empty_like(q)
+    if batch == 0:
+        return o
+    args = _lib.PagedArgs(
+        _lib.ptr(q), _lib.ptr(k_pages), _lib.ptr(v_pages), _lib.ptr(tables), _lib.ptr(lens),
+        _lib.ptr(o), batch, num_heads, num_kv_heads, num_pages, page_size, head_dim,
+        tables.shape[1], float(sm_scale), _lib.dtype_tag(q), None, 0)
+    L = _lib.lib()
+    ws_bytes = L.pf_paged_attn_workspace_size(args)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=dev)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = ws.numel()
+    with torch.cuda.device(dev):
+        _lib.check(L.pf_paged_attn(args, _lib.stream_of(q)), "paged_flash_attention")
+    return o
+
+
+def init_paged_cache(num_pages: int, num_kv_heads: int, page_size: int, head_dim: int,
+                     dtype=torch.float32, device=None):
+    """Allocate an empty page pool ``(k_pages, v_pages)`` (paged.py:198-202)."""
+    shape = (num_pages, num_kv_heads, page_size, head_dim)
+    return (torch.zeros(shape, dtype=dtype, device=device),
+            torch.zeros(shape, dtype=dtype, device=device))
+
+
+def write_to_paged_cache(k_pages, v_pages, k, v, block_table, position: int):
+    """Write one token's K/V into the page holding ``position`` (paged.py:205-223).
+
+    Args:
+        k, v: ``[1, num_kv_heads, 1, head_dim]`` for a single token.
+        block_table: ``[pages_per_seq]`` table of this sequence.
+        position: absolute token position being written.
+
+    Returns the updated ``(k_pages, v_pages)`` (updated in place and returned,
+    so the reference's functional call pattern keeps working).
+    """
+    page_size = k_pages.shape[2]
+    logical_page, offset = divmod(int(position), page_size)
+    physical_page = int(torch.as_tensor(block_table)[logical_page])
+    k_pages[physical_page, :, offset] = k[0, :, 0].to(k_pages.dtype)
+    v_pages[physical_page, :, offset] = v[0, :, 0].to(v_pages.dtype)
+    return k_pages, v_pages
+
+
+__all__ = ["paged_flash_attention", "init_paged_cache", "write_to_paged_cache"]
