@@ -103,7 +103,10 @@ constexpr int frags_per_chunk() {
 template <typename T>
 __device__ inline typename Mfma32<T>::Frag chunk_frag(const u32x4& c, int i) {
   if constexpr (sizeof(T) == 4) {
-    return __builtin_bit_cast(float, c[i]);
+    // Cast the whole vector, then index: this compiler mis-lowers
+    // __builtin_bit_cast(float, c[i]) on an ext-vector element (it reads
+    // element 0 for every i).
+    return __builtin_bit_cast(f32x4, c)[i];
   } else {
     return __builtin_bit_cast(typename Mfma32<T>::Frag, c);
   }
@@ -113,8 +116,9 @@ __device__ inline typename Mfma32<T>::Frag chunk_frag(const u32x4& c, int i) {
 template <typename T>
 __device__ inline void chunk_to_f32(const u32x4& c, float* out) {
   if constexpr (sizeof(T) == 4) {
+    const f32x4 x = __builtin_bit_cast(f32x4, c);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(float, c[i]);
+    for (int i = 0; i < 4; ++i) out[i] = x[i];
   } else {
     typedef T v8 __attribute__((ext_vector_type(8)));
     v8 x = __builtin_bit_cast(v8, c);
@@ -127,10 +131,8 @@ __device__ inline void chunk_to_f32(const u32x4& c, float* out) {
 template <typename T>
 __device__ inline u32x4 f32_to_chunk(const float* in) {
   if constexpr (sizeof(T) == 4) {
-    u32x4 c;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = __builtin_bit_cast(uint32_t, in[i]);
-    return c;
+    const f32x4 x = {in[0], in[1], in[2], in[3]};
+    return __builtin_bit_cast(u32x4, x);
   } else {
     typedef T v8 __attribute__((ext_vector_type(8)));
     v8 x;
