@@ -7,18 +7,25 @@
 // Work decomposition: one workgroup of 4 waves per (batch, query head, 128-row
 // query block); each wave owns 32 query rows. The grid is 1-D: heavy (late)
 // query blocks first for causal load balance, and the query heads of one GQA
-// group on one XCD so they hit the same L2 for K/V (see xcd_remap).
+// group on one XCD so they share K/V in that XCD's L2 (see xcd_remap).
 //
-// Per 64-key block: K [64 x D] is staged in LDS row-major; V is staged
-// transposed (V^T [D x 64]) because P.V contracts over keys and an MFMA
-// operand must hold its reduction index contiguously per lane.
+// Per 64-key block the workgroup stages K and V in LDS, double-buffered: the
+// global loads for block j+1 are in flight while block j is computed, and one
+// barrier per block separates the two buffers.
 //   S^T = K . Q^T   (A = K rows from LDS, B = Q held in registers)
-//   O^T += V^T . P^T (A = V^T rows from LDS, B = P from the S^T accumulators)
+//   O^T += V^T . P^T (A = V^T fragments from LDS, B = P from the S^T accumulators)
 // With S^T, lane l owns query l%32: the online-softmax row statistics are
 // in-lane except one exchange between the two lane halves. K rows are stored
-// in LDS in a permuted order so that lane half hh's 32 accumulator values
-// are keys [32hh, 32hh+32) of the block in order, exactly the k-slots the
-// P^T operand needs -- no cross-lane shuffle of P.
+// in LDS in a permuted order so that lane half hh's 32 accumulator values are
+// keys [32hh, 32hh+32) of the block, exactly the k-slots the P^T operand
+// needs -- P never moves between lanes.
+// V^T fragments: for 16-bit types V stays row-major in LDS and is read with
+// the gfx950 transposing LDS load (ds_read_b64_tr_b16: within each 16-lane
+// group, lane i receives element [4t + i/4][i%4] of the 16 x 4 block the group
+// addressed, so lane j pointing at V[k0 + j/4][d0 + 4(j%4)] hands lane i the
+// values V[k0 + t][d0 + i]). For float32 V is staged transposed.
+// LDS tiles are unpadded with 16-byte chunks XOR-swizzled per row so the MFMA
+// reads and the staging writes are free of bank conflicts.
 //
 // Semantics (flash_attention.py): mask k >= kv_len and (causal) k > q, with
 // K/V rows past kv_len never read (zero-filled) (:95-120); online softmax in
@@ -28,6 +35,7 @@
 // into the scale) and converted back for the LSE.
 #include "pf_common.hpp"
 #include "pf_kernels.hpp"
+#include "pf_tiles.hpp"
 
 namespace pf {
 
@@ -36,33 +44,40 @@ namespace {
 constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdBN = 64;   // keys per block
 
-// LDS row of key r (0..63) inside a staged K block: MFMA tile t = (r>>4)&1 row
-// 8*((r>>2)&3) + 4*(r>>5) + (r&3). Lane half hh then reads back keys
-// 32hh + 16t + reg for accumulator register `reg`.
-__device__ inline int k_lds_row(int r) {
-  return ((r >> 4) & 1) * 32 + ((r >> 2) & 3) * 8 + (r >> 5) * 4 + (r & 3);
-}
+template <typename T, int D, bool ROPE>
+struct FwdTiles {
+  static constexpr int ES = sizeof(T);
+  static constexpr int EPC = 16 / ES;         // elements per 16-byte chunk
+  static constexpr int CPR = D / EPC;         // chunks per row
+  static constexpr bool TR = (ES == 2);       // transposing LDS reads for V
+  static constexpr int K_BYTES = kFwdBN * D * ES;
+  static constexpr int VT_PITCH = kFwdBN * ES + 16;
+  static constexpr int V_BYTES = TR ? kFwdBN * D * ES : D * VT_PITCH;
+  static constexpr int K_ITEMS = ROPE ? kFwdBN * CPR / 2 : kFwdBN * CPR;   // per block
+  static constexpr int K_PER_T = (K_ITEMS + 255) / 256;
+  static constexpr int K_CHUNKS = ROPE ? 2 : 1;                             // chunks per item
+  static constexpr int V_ITEMS = TR ? kFwdBN * CPR : 16 * CPR;              // f32: 4-row groups
+  static constexpr int V_PER_T = (V_ITEMS + 255) / 256;
+  static constexpr int V_CHUNKS = TR ? 1 : 4;
+  // 16-byte chunk swizzles (row-dependent XOR keeps each row's chunks in place)
+  __device__ static int kswz(int row) { return row & (CPR >= 16 ? 15 : CPR - 1); }
+  __device__ static int vswz(int row) { return CPR >= 16 ? 4 * (row & 3) : 4 * (row & 1); }
+};
 
 template <typename T, int D, bool CAUSAL, bool ROPE>
-__global__ __launch_bounds__(256, 2) void pf_attn_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_attn_fwd_kernel(FwdParams p) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
+  using G = FwdTiles<T, D, ROPE>;
   constexpr int BM = kFwdBM, BN = kFwdBN;
   constexpr int HALF = D / 2;
-  constexpr int ES = sizeof(T);
-  constexpr int EPC = 16 / ES;   // elements per 16-byte chunk
-  constexpr int CPR = D / EPC;   // chunks per row
-  constexpr int KP = D * ES + 16;   // K tile row pitch (bytes)
-  constexpr int VP = BN * ES + 16;  // V^T tile row pitch (bytes)
+  constexpr int ES = G::ES, EPC = G::EPC, CPR = G::CPR;
   constexpr int FPC = frags_per_chunk<T>();
   constexpr int QF = HALF / MF::kK;  // Q fragments per lane
   constexpr int NDT = D / 32;        // 32-row tiles of O^T
   constexpr int PF = 32 / MF::kK;    // P fragments per lane per block
-  static_assert(BM == 128 && BN == 64, "tile shape is baked into the lane maps");
 
-  __shared__ __attribute__((aligned(16))) char smem[BN * KP + D * VP];
-  char* const sk = smem;
-  char* const sv = smem + BN * KP;
+  __shared__ __attribute__((aligned(16))) char smem[2 * (G::K_BYTES + G::V_BYTES)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -124,44 +139,57 @@ __global__ __launch_bounds__(256, 2) void pf_attn_fwd_kernel(FwdParams p) {
       for (int f = 0; f < FPC; ++f) qf[c * FPC + f] = chunk_frag<T>(qc[c], f);
   }
 
-  float m_run = kNegInf;  // running max, log2 domain (identical in both halves)
-  float l_run = 0.f;      // running sum over this lane half's keys
-  f32x16 acc[NDT];
+  // ---- staging registers for one K/V block ---------------------------------
+  u32x4 kreg[G::K_PER_T][G::K_CHUNKS];
+  u32x4 vreg[G::V_PER_T][G::V_CHUNKS];
+
+  auto load_block = [&](int kv0) {
 #pragma unroll
-  for (int i = 0; i < NDT; ++i) acc[i] = (f32x16)(0.f);
-
-  int kv_end = p.kv_len;
-  if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + BM, p.Sq));
-  const int nblk = (kv_end + BN - 1) / BN;
-
-  for (int j = 0; j < nblk; ++j) {
-    const int kv0 = j * BN;
-    __syncthreads();  // previous block's LDS reads are done
-
-    // ---- stage K (row-permuted) -------------------------------------------
-    if constexpr (!ROPE) {
-#pragma unroll
-      for (int u = 0; u < BN * CPR / 256; ++u) {
-        const int c = tid + 256 * u;
-        const int r = c / CPR, cc = c % CPR;
+    for (int u = 0; u < G::K_PER_T; ++u) {
+      const int c = tid + 256 * u;
+      if (G::K_ITEMS % 256 == 0 || c < G::K_ITEMS) {
+        const int r = ROPE ? c / (CPR / 2) : c / CPR;
+        const int cc = ROPE ? c % (CPR / 2) : c % CPR;
         const int key = kv0 + r;
-        const u32x4 val = (key < p.kv_len) ? ldg16(Kb + (int64_t)key * D + cc * EPC)
-                                           : (u32x4){0u, 0u, 0u, 0u};
-        sts16(sk + k_lds_row(r) * KP + cc * 16, val);
+        const bool ok = key < p.kv_len;
+        const T* src = Kb + (int64_t)key * D + cc * EPC;
+        kreg[u][0] = ok ? ldg16(src) : (u32x4){0u, 0u, 0u, 0u};
+        if constexpr (ROPE) kreg[u][G::K_CHUNKS - 1] = ok ? ldg16(src + HALF) : (u32x4){0u, 0u, 0u, 0u};
       }
-    } else {
-      constexpr int HC = CPR / 2;  // chunks per half row
+    }
 #pragma unroll
-      for (int u = 0; u < (BN * HC + 255) / 256; ++u) {
-        const int c = tid + 256 * u;
-        if (BN * HC % 256 == 0 || c < BN * HC) {
-          const int r = c / HC, pc = c % HC;
+    for (int u = 0; u < G::V_PER_T; ++u) {
+      const int c = tid + 256 * u;
+      if (G::V_ITEMS % 256 == 0 || c < G::V_ITEMS) {
+        if constexpr (G::TR) {
+          const int r = c / CPR, cc = c % CPR;
+          const int key = kv0 + r;
+          vreg[u][0] = key < p.kv_len ? ldg16(Vb + (int64_t)key * D + cc * EPC) : (u32x4){0u, 0u, 0u, 0u};
+        } else {
+          const int kg = c & 15, dc = c >> 4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kv0 + 4 * kg + r;
+            vreg[u][r] = key < p.kv_len ? ldg16(Vb + (int64_t)key * D + dc * EPC) : (u32x4){0u, 0u, 0u, 0u};
+          }
+        }
+      }
+    }
+  };
+
+  auto store_block = [&](int kv0, char* sk, char* sv) {
+#pragma unroll
+    for (int u = 0; u < G::K_PER_T; ++u) {
+      const int c = tid + 256 * u;
+      if (G::K_ITEMS % 256 == 0 || c < G::K_ITEMS) {
+        if constexpr (ROPE) {
+          const int r = c / (CPR / 2), pc = c % (CPR / 2);
           const int key = kv0 + r;
           u32x4 lo_out = {0u, 0u, 0u, 0u}, hi_out = {0u, 0u, 0u, 0u};
           if (key < p.kv_len) {
             float lo[EPC], hi[EPC], rlo[EPC], rhi[EPC];
-            chunk_to_f32<T>(ldg16(Kb + (int64_t)key * D + pc * EPC), lo);
-            chunk_to_f32<T>(ldg16(Kb + (int64_t)key * D + HALF + pc * EPC), hi);
+            chunk_to_f32<T>(kreg[u][0], lo);
+            chunk_to_f32<T>(kreg[u][1], hi);
             const float* cs = p.k_cos + (int64_t)key * D + pc * EPC;
             const float* sn = p.k_sin + (int64_t)key * D + pc * EPC;
 #pragma unroll
@@ -172,139 +200,180 @@ __global__ __launch_bounds__(256, 2) void pf_attn_fwd_kernel(FwdParams p) {
             lo_out = f32_to_chunk<T>(rlo);
             hi_out = f32_to_chunk<T>(rhi);
           }
-          char* dst = sk + k_lds_row(r) * KP;
-          sts16(dst + pc * 16, lo_out);
-          sts16(dst + (pc + HC) * 16, hi_out);
+          const int pr = perm_row(r);
+          char* dst = sk + pr * (D * ES);
+          sts16(dst + 16 * (pc ^ G::kswz(pr)), lo_out);
+          sts16(dst + 16 * ((pc + CPR / 2) ^ G::kswz(pr)), hi_out);
+        } else {
+          const int r = c / CPR, cc = c % CPR;
+          const int pr = perm_row(r);
+          sts16(sk + pr * (D * ES) + 16 * (cc ^ G::kswz(pr)), kreg[u][0]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < G::V_PER_T; ++u) {
+      const int c = tid + 256 * u;
+      if (G::V_ITEMS % 256 == 0 || c < G::V_ITEMS) {
+        if constexpr (G::TR) {
+          const int r = c / CPR, cc = c % CPR;
+          sts16(sv + r * (D * ES) + 16 * (cc ^ G::vswz(r)), vreg[u][0]);
+        } else {
+          const int kg = c & 15, dc = c >> 4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const u32x4 o4 = {vreg[u][0][e], vreg[u][1][e], vreg[u][2][e], vreg[u][3][e]};
+            sts16(sv + (dc * 4 + e) * G::VT_PITCH + kg * 16, o4);
+          }
+        }
+      }
+    }
+  };
+
+  float m_run = kNegInf;  // running max, log2 domain (identical in both halves)
+  float l_run = 0.f;      // running sum over this lane half's keys
+  f32x16 acc[NDT];
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) acc[i] = (f32x16)(0.f);
+
+  int kv_end = p.kv_len;
+  if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + BM, p.Sq));
+  const int nblk = (kv_end + BN - 1) / BN;
+  const float c2 = p.scale_log2;
+
+  // per-lane constants of the V^T fragment reads (16-bit types)
+  const int tr_g = lane >> 4, tr_j = lane & 15;
+  const int tr_row0 = 32 * (tr_g >> 1) + (tr_j >> 2);          // + 8c + 4r
+  const int tr_col0 = 16 * (tr_g & 1) + 4 * (tr_j & 3);        // + 32dt (elements)
+
+  if (nblk > 0) {
+    load_block(0);
+    store_block(0, smem, smem + G::K_BYTES);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nblk; ++j) {
+    const int kv0 = j * BN;
+    char* const sk = smem + (j & 1) * (G::K_BYTES + G::V_BYTES);
+    char* const sv = sk + G::K_BYTES;
+    const bool has_next = j + 1 < nblk;
+    if (has_next) load_block(kv0 + BN);
+
+    const bool live = wq0 < p.Sq && !(CAUSAL && kv0 > wq_last);
+    if (live) {
+      // ---- S^T = K . Q^T --------------------------------------------------
+      f32x16 s[2];
+      s[0] = (f32x16)(0.f);
+      s[1] = (f32x16)(0.f);
+      {
+        const char* kr0 = sk + l32 * (D * ES);
+        const char* kr1 = sk + (32 + l32) * (D * ES);
+        const int sw0 = G::kswz(l32), sw1 = G::kswz(32 + l32);
+#pragma unroll
+        for (int c = 0; c < HALF / EPC; ++c) {
+          const int ch = hh * (CPR / 2) + c;
+          const u32x4 a0 = lds16(kr0 + 16 * (ch ^ sw0));
+          const u32x4 a1 = lds16(kr1 + 16 * (ch ^ sw1));
+#pragma unroll
+          for (int f = 0; f < FPC; ++f) {
+            s[0] = MF::run(chunk_frag<T>(a0, f), qf[c * FPC + f], s[0]);
+            s[1] = MF::run(chunk_frag<T>(a1, f), qf[c * FPC + f], s[1]);
+          }
+        }
+      }
+
+      // ---- online softmax (lane owns query qrow; keys kv0 + 32hh + 16t + r)
+      const bool need_mask = (kv0 + BN > p.kv_len) || (CAUSAL && kv0 + BN - 1 > wq0);
+      if (need_mask) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + 32 * hh + 16 * t + r;
+            const bool ok = key < p.kv_len && (!CAUSAL || key <= qrow);
+            s[t][r] = ok ? s[t][r] : kNegInf;
+          }
+      }
+      float mx = kNegInf;
+      if (c2 > 0.f) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+        mx = wave_xor32_max(mx) * c2;
+      } else {
+        // non-positive scale: scale first (the ordering flips), keep masks at -inf
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            s[t][r] = s[t][r] == kNegInf ? kNegInf : s[t][r] * c2;
+            mx = fmaxf(mx, s[t][r]);
+          }
+        mx = wave_xor32_max(mx);
+      }
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      const float cs = c2 > 0.f ? c2 : 1.f;
+      float rs = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[t][r], cs, -m_use));
+          s[t][r] = e;
+          rs += e;
+        }
+      l_run = l_run * alpha + rs;
+      m_run = m_new;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int i = 0; i < NDT; ++i) acc[i] *= alpha;
+      }
+
+      // ---- P fragments (B operand of O^T): keys 32hh + m, m = 0..31 --------
+      Frag pfr[PF];
+      pack_frags<T>(s[0], s[1], pfr);
+
+      // ---- O^T += V^T . P^T -------------------------------------------------
+      if constexpr (G::TR) {
+        typedef short v4i16 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v4i16 part[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const int row = tr_row0 + 8 * c + 4 * r;
+              const int col = 32 * dt + tr_col0;
+              const char* a = sv + row * (D * ES) + 16 * ((col >> 3) ^ G::vswz(row)) + 2 * (col & 7);
+              part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (__attribute__((address_space(3))) v4i16*)(a));
+            }
+            const Frag af = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[dt] = MF::run(af, pfr[c], acc[dt]);
+          }
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const char* vr = sv + (32 * dt + l32) * G::VT_PITCH + hh * 32 * ES;
+#pragma unroll
+          for (int c = 0; c < 32 * ES / 16; ++c) {
+            const u32x4 a = lds16(vr + c * 16);
+#pragma unroll
+            for (int f = 0; f < FPC; ++f) acc[dt] = MF::run(chunk_frag<T>(a, f), pfr[c * FPC + f], acc[dt]);
+          }
         }
       }
     }
 
-    // ---- stage V transposed: V^T[d][key] ----------------------------------
-    {
-      constexpr int NDC = D / EPC;
-#pragma unroll
-      for (int u = 0; u < (16 * NDC + 255) / 256; ++u) {
-        const int c = tid + 256 * u;
-        if (16 * NDC % 256 == 0 || c < 16 * NDC) {
-          const int kg = c & 15, dc = c >> 4;
-          u32x4 ch[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = kv0 + 4 * kg + r;
-            ch[r] = (key < p.kv_len) ? ldg16(Vb + (int64_t)key * D + dc * EPC)
-                                     : (u32x4){0u, 0u, 0u, 0u};
-          }
-          if constexpr (ES == 4) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const u32x4 o4 = {ch[0][e], ch[1][e], ch[2][e], ch[3][e]};
-              sts16(sv + (dc * 4 + e) * VP + kg * 16, o4);
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int wd = e >> 1, sh = (e & 1) * 16;
-              const uint32_t v0 = (ch[0][wd] >> sh) & 0xffffu, v1 = (ch[1][wd] >> sh) & 0xffffu;
-              const uint32_t v2 = (ch[2][wd] >> sh) & 0xffffu, v3 = (ch[3][wd] >> sh) & 0xffffu;
-              const u32x2 o2 = {v0 | (v1 << 16), v2 | (v3 << 16)};
-              *reinterpret_cast<u32x2*>(sv + (dc * 8 + e) * VP + kg * 8) = o2;
-            }
-          }
-        }
-      }
+    if (has_next) {
+      char* const nk = smem + ((j + 1) & 1) * (G::K_BYTES + G::V_BYTES);
+      store_block(kv0 + BN, nk, nk + G::K_BYTES);
     }
     __syncthreads();
-
-    if (wq0 >= p.Sq) continue;                // wave has no query rows
-    if (CAUSAL && kv0 > wq_last) continue;    // block entirely in this wave's future
-
-    // ---- S^T = K . Q^T ----------------------------------------------------
-    f32x16 s[2];
-    s[0] = (f32x16)(0.f);
-    s[1] = (f32x16)(0.f);
-    {
-      const char* kr0 = sk + l32 * KP + hh * HALF * ES;
-      const char* kr1 = sk + (32 + l32) * KP + hh * HALF * ES;
-#pragma unroll
-      for (int c = 0; c < HALF / EPC; ++c) {
-        const u32x4 a0 = lds16(kr0 + c * 16);
-        const u32x4 a1 = lds16(kr1 + c * 16);
-#pragma unroll
-        for (int f = 0; f < FPC; ++f) {
-          s[0] = MF::run(chunk_frag<T>(a0, f), qf[c * FPC + f], s[0]);
-          s[1] = MF::run(chunk_frag<T>(a1, f), qf[c * FPC + f], s[1]);
-        }
-      }
-    }
-
-    // ---- online softmax (lane owns query qrow; keys kv0 + 32hh + 16t + r) --
-    const bool need_mask = (kv0 + BN > p.kv_len) || (CAUSAL && kv0 + BN - 1 > wq0);
-    float mx = kNegInf;
-    if (need_mask) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kv0 + 32 * hh + 16 * t + r;
-          const bool ok = key < p.kv_len && (!CAUSAL || key <= qrow);
-          const float x = ok ? s[t][r] * p.scale_log2 : kNegInf;
-          s[t][r] = x;
-          mx = fmaxf(mx, x);
-        }
-    } else {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = s[t][r] * p.scale_log2;
-          s[t][r] = x;
-          mx = fmaxf(mx, x);
-        }
-    }
-    mx = wave_xor32_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    float rs = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = exp2f(s[t][r] - m_use);
-        s[t][r] = e;
-        rs += e;
-      }
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < NDT; ++i) acc[i] *= alpha;
-
-    // ---- P fragments (B operand of O^T): keys 32hh + m, m = 0..31 ----------
-    Frag pfr[PF];
-    if constexpr (ES == 4) {
-#pragma unroll
-      for (int m = 0; m < 32; ++m) pfr[m] = s[m >> 4][m & 15];
-    } else {
-#pragma unroll
-      for (int f = 0; f < PF; ++f) {
-        Frag x;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = Elem<T>::from_f32(s[f >> 1][8 * (f & 1) + e]);
-        pfr[f] = x;
-      }
-    }
-
-    // ---- O^T += V^T . P^T ---------------------------------------------------
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const char* vr = sv + (32 * dt + l32) * VP + hh * 32 * ES;
-#pragma unroll
-      for (int c = 0; c < 32 * ES / 16; ++c) {
-        const u32x4 a = lds16(vr + c * 16);
-#pragma unroll
-        for (int f = 0; f < FPC; ++f) acc[dt] = MF::run(chunk_frag<T>(a, f), pfr[c * FPC + f], acc[dt]);
-      }
-    }
   }
 
   // ---- finalize: o = acc / l, lse = m ln2 + ln l ---------------------------

@@ -52,7 +52,7 @@ __device__ inline const T* key_row(const DecodeParams& p, const T* base, int b, 
 }
 
 template <typename T, int D, bool PAGED>
-__global__ __launch_bounds__(256, 2) void pf_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_decode_kernel(DecodeParams p) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
   constexpr int BN = kDecBN;
