@@ -133,6 +133,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 #pragma unroll
       for (int c = 0; c < HALF / EPC; ++c) qc[c] = (u32x4){0u, 0u, 0u, 0u};
     }
+    // A negative scale is applied as |scale| on -Q (exact sign flips), so the
+    // softmax below only ever sees a non-negative scale.
+    if (p.scale_log2 < 0.f) {
+      const uint32_t sign = ES == 4 ? 0x80000000u : 0x80008000u;
+#pragma unroll
+      for (int c = 0; c < HALF / EPC; ++c) qc[c] ^= (u32x4){sign, sign, sign, sign};
+    }
 #pragma unroll
     for (int c = 0; c < HALF / EPC; ++c)
 #pragma unroll
@@ -143,6 +150,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   u32x4 kreg[G::K_PER_T][G::K_CHUNKS];
   u32x4 vreg[G::V_PER_T][G::V_CHUNKS];
 
+  // K/V of this (batch, kv head): rows at or past kv_len lie outside the
+  // resource and load as zeros (never read from memory).
+  const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
+  const rsrc_t krs = make_rsrc(Kb, kv_bytes);
+  const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
+
   auto load_block = [&](int kv0) {
 #pragma unroll
     for (int u = 0; u < G::K_PER_T; ++u) {
@@ -150,11 +163,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       if (G::K_ITEMS % 256 == 0 || c < G::K_ITEMS) {
         const int r = ROPE ? c / (CPR / 2) : c / CPR;
         const int cc = ROPE ? c % (CPR / 2) : c % CPR;
-        const int key = kv0 + r;
-        const bool ok = key < p.kv_len;
-        const T* src = Kb + (int64_t)key * D + cc * EPC;
-        kreg[u][0] = ok ? ldg16(src) : (u32x4){0u, 0u, 0u, 0u};
-        if constexpr (ROPE) kreg[u][G::K_CHUNKS - 1] = ok ? ldg16(src + HALF) : (u32x4){0u, 0u, 0u, 0u};
+        const uint32_t off = (uint32_t)((kv0 + r) * D + cc * EPC) * ES;
+        kreg[u][0] = bufld16(krs, off);
+        if constexpr (ROPE) kreg[u][G::K_CHUNKS - 1] = bufld16(krs, off + HALF * ES);
       }
     }
 #pragma unroll
@@ -163,15 +174,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       if (G::V_ITEMS % 256 == 0 || c < G::V_ITEMS) {
         if constexpr (G::TR) {
           const int r = c / CPR, cc = c % CPR;
-          const int key = kv0 + r;
-          vreg[u][0] = key < p.kv_len ? ldg16(Vb + (int64_t)key * D + cc * EPC) : (u32x4){0u, 0u, 0u, 0u};
+          vreg[u][0] = bufld16(vrs, (uint32_t)((kv0 + r) * D + cc * EPC) * ES);
         } else {
           const int kg = c & 15, dc = c >> 4;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = kv0 + 4 * kg + r;
-            vreg[u][r] = key < p.kv_len ? ldg16(Vb + (int64_t)key * D + dc * EPC) : (u32x4){0u, 0u, 0u, 0u};
-          }
+          for (int r = 0; r < 4; ++r)
+            vreg[u][r] = bufld16(vrs, (uint32_t)((kv0 + 4 * kg + r) * D + dc * EPC) * ES);
         }
       }
     }
@@ -186,7 +194,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
           const int r = c / (CPR / 2), pc = c % (CPR / 2);
           const int key = kv0 + r;
           u32x4 lo_out = {0u, 0u, 0u, 0u}, hi_out = {0u, 0u, 0u, 0u};
-          if (key < p.kv_len) {
+          if (key < p.kv_len) {  // tables are [Sk, D]: only read for valid keys
             float lo[EPC], hi[EPC], rlo[EPC], rhi[EPC];
             chunk_to_f32<T>(kreg[u][0], lo);
             chunk_to_f32<T>(kreg[u][1], hi);
@@ -239,12 +247,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   int kv_end = p.kv_len;
   if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + BM, p.Sq));
   const int nblk = (kv_end + BN - 1) / BN;
-  const float c2 = p.scale_log2;
+  const float c2 = fabsf(p.scale_log2);
 
-  // per-lane constants of the V^T fragment reads (16-bit types)
+  // Per-lane byte offsets of the V^T fragment reads (16-bit types). Lane
+  // (group gq = lane/16, j = lane%16) points at V[32(gq/2) + 8c + 4r + j/4]
+  // [32dt + 16(gq%2) + 4(j%4)]; the row swizzle only depends on row%4 =
+  // (j/4)%4, so the per-dt chunk offsets are lane constants.
   const int tr_g = lane >> 4, tr_j = lane & 15;
-  const int tr_row0 = 32 * (tr_g >> 1) + (tr_j >> 2);          // + 8c + 4r
-  const int tr_col0 = 16 * (tr_g & 1) + 4 * (tr_j & 3);        // + 32dt (elements)
+  const int tr_row0 = 32 * (tr_g >> 1) + (tr_j >> 2);
+  const int tr_col0 = 16 * (tr_g & 1) + 4 * (tr_j & 3);
+  const int tr_sw = G::TR ? G::vswz(tr_row0) : 0;
+  const int tr_base = tr_row0 * (D * ES) + 16 * (tr_col0 >> 3) + 2 * (tr_col0 & 7);
+  int tr_dt[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) tr_dt[dt] = tr_base + 16 * ((4 * dt) ^ tr_sw);
 
   if (nblk > 0) {
     load_block(0);
@@ -283,7 +299,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       }
 
       // ---- online softmax (lane owns query qrow; keys kv0 + 32hh + 16t + r)
+      // c2 = |scale| * log2(e) >= 0. The running reference m_run only moves
+      // when some row's max grows by more than 8 (log2 units): p = 2^(x - m)
+      // then stays below 2^8, and since l and acc share the reference the
+      // result is unchanged while the O rescale becomes rare.
       const bool need_mask = (kv0 + BN > p.kv_len) || (CAUSAL && kv0 + BN - 1 > wq0);
+      float mx = kNegInf;
       if (need_mask) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -291,46 +312,48 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
           for (int r = 0; r < 16; ++r) {
             const int key = kv0 + 32 * hh + 16 * t + r;
             const bool ok = key < p.kv_len && (!CAUSAL || key <= qrow);
-            s[t][r] = ok ? s[t][r] : kNegInf;
+            mx = fmaxf(mx, ok ? s[t][r] : kNegInf);
           }
-      }
-      float mx = kNegInf;
-      if (c2 > 0.f) {
+      } else {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-        mx = wave_xor32_max(mx) * c2;
-      } else {
-        // non-positive scale: scale first (the ordering flips), keep masks at -inf
+      }
+      mx = wave_xor32_max(mx);
+      mx = (mx == kNegInf) ? kNegInf : mx * c2;
+      const float m_cand = fmaxf(m_run, mx);
+      if (__any(m_cand > m_run + 8.f)) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+#pragma unroll
+        for (int i = 0; i < NDT; ++i) acc[i] *= alpha;
+        l_run *= alpha;
+        m_run = m_cand;
+      }
+      const float m_use = (m_run == kNegInf) ? 0.f : m_run;
+      float rs = 0.f;
+      if (need_mask) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            s[t][r] = s[t][r] == kNegInf ? kNegInf : s[t][r] * c2;
-            mx = fmaxf(mx, s[t][r]);
+            const int key = kv0 + 32 * hh + 16 * t + r;
+            const bool ok = key < p.kv_len && (!CAUSAL || key <= qrow);
+            const float e = ok ? __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_use)) : 0.f;
+            s[t][r] = e;
+            rs += e;
           }
-        mx = wave_xor32_max(mx);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float e = __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_use));
+            s[t][r] = e;
+            rs += e;
+          }
       }
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      const float cs = c2 > 0.f ? c2 : 1.f;
-      float rs = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(s[t][r], cs, -m_use));
-          s[t][r] = e;
-          rs += e;
-        }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int i = 0; i < NDT; ++i) acc[i] *= alpha;
-      }
+      l_run += rs;
 
       // ---- P fragments (B operand of O^T): keys 32hh + m, m = 0..31 --------
       Frag pfr[PF];
@@ -346,9 +369,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
             v4i16 part[2];
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-              const int row = tr_row0 + 8 * c + 4 * r;
-              const int col = 32 * dt + tr_col0;
-              const char* a = sv + row * (D * ES) + 16 * ((col >> 3) ^ G::vswz(row)) + 2 * (col & 7);
+              const char* a = sv + tr_dt[dt] + (8 * c + 4 * r) * (D * ES);
               part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                   (__attribute__((address_space(3))) v4i16*)(a));
             }

@@ -50,6 +50,8 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   p->n_qblk = (a->seq_len_q + 127) / 128;
   const int64_t n_work = (int64_t)a->batch * a->num_heads * p->n_qblk;
   if (n_work > kMaxGrid) return PF_ERR_UNSUPPORTED;
+  // per-(batch, kv head) byte offsets are 32-bit inside the kernels
+  if ((int64_t)(a->seq_len_k + 256) * a->head_dim * 4 > 0x7fffffff) return PF_ERR_UNSUPPORTED;
   p->n_work = (int)n_work;
   return PF_OK;
 }

@@ -142,6 +142,17 @@ __device__ inline u32x4 f32_to_chunk(const float* in) {
   }
 }
 
+// Raw buffer resource over [base, base + bytes): loads at byte offsets at or
+// past `bytes` return zeros without touching memory (hardware bounds check),
+// which is how rows past kv_len are zero-filled without branches.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ inline u32x4 bufld16(rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
+}
+
 __device__ inline u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void stg16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ inline u32x4 lds16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
