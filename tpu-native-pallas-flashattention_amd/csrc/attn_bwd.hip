@@ -13,14 +13,17 @@
 // per-head float32 [B, Hq, Sk, D] temporaries and the separate sum pass do
 // not exist here.
 //
-// Layouts (all 32x32 MFMA, float32 accumulation):
-//  dQ kernel (workgroup = 128 query rows, 4 waves x 32 rows; loop over 64-key
-//  blocks): S^T = K Q^T, dP^T = V dO^T (K, V natural in LDS; Q, dO in
-//  registers); dS^T = P^T (dP^T - delta); dQ^T += K^T dS^T (K^T in LDS).
-//  dK/dV kernel (workgroup = 128 keys, 4 waves x 32 keys; loop over group
-//  heads x 64-row query blocks): S = Q K^T, dP = dO V^T (Q, dO natural in
-//  LDS; K, V in registers); dS = P (dP - delta); dV^T += dO^T P,
-//  dK^T += Q^T dS (Q^T, dO^T transposed in LDS).
+// Both kernels use the forward's pipeline: 64-row LDS tiles staged with
+// bounds-checked buffer loads, double-buffered with one barrier per step, and
+// every transposed operand read from the single natural copy with the
+// transposing LDS load (pf_tiles.hpp).
+//  dQ (workgroup = 128 query rows, 4 waves x 32 rows; loop over 64-key blocks):
+//    S^T = K Q^T, dP^T = V dO^T  (K, V tiles; Q, dO in registers)
+//    dS^T = P^T (dP^T - delta);  dQ^T += K^T dS^T  (K^T from the K tile)
+//  dK/dV (workgroup = 128 keys, 4 waves x 32 keys; loop over the group's
+//  heads x 64-row query blocks):
+//    S = Q K^T, dP = dO V^T  (Q, dO tiles; K, V in registers)
+//    dS = P (dP - delta);  dV^T += dO^T P,  dK^T += Q^T dS  (from the same tiles)
 #include "pf_common.hpp"
 #include "pf_kernels.hpp"
 #include "pf_tiles.hpp"
@@ -57,19 +60,18 @@ __global__ __launch_bounds__(256) void pf_attn_bwd_delta_kernel(BwdParams p) {
 // dQ
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
+__global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2)
+void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
-  using G = TileGeom<T, D>;
+  using G = Tile<T, D>;
   constexpr int BM = 128, BN = 64;
   constexpr int QF = (D / 2) / MF::kK;
   constexpr int NDT = D / 32;
   constexpr int PF = 32 / MF::kK;
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * G::NAT_BYTES + G::TRN_BYTES];
-  char* const sk = smem;
-  char* const sv = smem + G::NAT_BYTES;
-  char* const skt = smem + 2 * G::NAT_BYTES;
+  // two buffers x (K tile, V tile)
+  __shared__ __attribute__((aligned(16))) char smem[4 * G::BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
   const int w = xcd_remap(blockIdx.x, n_work, p.g);
@@ -103,39 +105,66 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dq_kernel(BwdParams p, int
 #pragma unroll
   for (int i = 0; i < NDT; ++i) acc[i] = (f32x16)(0.f);
 
+  const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)G::RB;
+  const rsrc_t krs = make_rsrc(Kb, kv_bytes);
+  const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
+  TileRegs<T, D> kreg, vreg;
+  TrAddr<T, D> kta;
+  kta.init(lane);
+
   int kv_end = p.kv_len;
   if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + BM, p.Sq));
   const int nblk = (kv_end + BN - 1) / BN;
 
+  if (nblk > 0) {
+    kreg.load(krs, 0, tid);
+    vreg.load(vrs, 0, tid);
+    kreg.store(smem, tid);
+    vreg.store(smem + G::BYTES, tid);
+  }
+  __syncthreads();
+
   for (int j = 0; j < nblk; ++j) {
     const int kv0 = j * BN;
-    __syncthreads();
-    stage_tile<T, D>(Kb, kv0, p.kv_len, sk, skt, tid);
-    stage_tile<T, D>(Vb, kv0, p.kv_len, sv, nullptr, tid);
-    __syncthreads();
-    if (wq0 >= p.Sq) continue;
-    if (CAUSAL && kv0 > wq_last) continue;
+    const char* sk = smem + (j & 1) * (2 * G::BYTES);
+    const char* sv = sk + G::BYTES;
+    const bool has_next = j + 1 < nblk;
+    if (has_next) {
+      kreg.load(krs, kv0 + BN, tid);
+      vreg.load(vrs, kv0 + BN, tid);
+    }
+    if (wq0 < p.Sq && !(CAUSAL && kv0 > wq_last)) {
+      f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f), d0 = (f32x16)(0.f), d1 = (f32x16)(0.f);
+      mfma_nat<T, D>(sk, l32, hh, qf, s0, s1);
+      mfma_nat<T, D>(sv, l32, hh, dof, d0, d1);
 
-    f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f), d0 = (f32x16)(0.f), d1 = (f32x16)(0.f);
-    mfma_rows_x_frags<T, D>(sk, l32, hh, qf, s0, s1);
-    mfma_rows_x_frags<T, D>(sv, l32, hh, dof, d0, d1);
-
-    // keys kv0 + 32hh + 16t + r, query qrow
+      // keys kv0 + 32hh + 16t + r, query qrow
+      const bool need_mask = !qvalid || (kv0 + BN > p.kv_len) || (CAUSAL && kv0 + BN - 1 > wq0);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kv0 + 32 * hh + 16 * t + r;
-        const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
-        const float sx = t ? s1[r] : s0[r];
-        const float dp = t ? d1[r] : d0[r];
-        const float pv = ok ? exp2f(sx * p.scale_log2 - lse2) : 0.f;
-        const float ds = pv * (dp - dlt);
-        if (t) s1[r] = ds; else s0[r] = ds;
-      }
-    Frag dsf[PF];
-    pack_frags<T>(s0, s1, dsf);
-    mfma_trn_x_frags<T, D>(skt, l32, hh, dsf, acc);
+        for (int r = 0; r < 16; ++r) {
+          const float sx = t ? s1[r] : s0[r];
+          const float dp = t ? d1[r] : d0[r];
+          float pv = __builtin_amdgcn_exp2f(fmaf(sx, p.scale_log2, -lse2));
+          if (need_mask) {
+            const int key = kv0 + 32 * hh + 16 * t + r;
+            const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
+            pv = ok ? pv : 0.f;
+          }
+          const float ds = pv * (dp - dlt);
+          if (t) s1[r] = ds; else s0[r] = ds;
+        }
+      Frag dsf[PF];
+      pack_frags<T>(s0, s1, dsf);
+      mfma_trn<T, D>(sk, lane, kta, dsf, acc);
+    }
+    if (has_next) {
+      char* nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
+      kreg.store(nk, tid);
+      vreg.store(nk + G::BYTES, tid);
+    }
+    __syncthreads();
   }
 
   if (qvalid) store_acc_row<T, D>(static_cast<T*>(p.dq) + (qoff + qrow) * D, acc, p.sm_scale, hh);
@@ -148,19 +177,15 @@ template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, int n_kblk) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
-  using G = TileGeom<T, D>;
+  using G = Tile<T, D>;
   constexpr int BNK = 128, BMQ = 64;
   constexpr int KF = (D / 2) / MF::kK;
   constexpr int NDT = D / 32;
   constexpr int PF = 32 / MF::kK;
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * G::NAT_BYTES + 2 * G::TRN_BYTES + 2 * BMQ * 4];
-  char* const sq = smem;
-  char* const sdo = smem + G::NAT_BYTES;
-  char* const sqt = smem + 2 * G::NAT_BYTES;
-  char* const sdot = smem + 2 * G::NAT_BYTES + G::TRN_BYTES;
-  float* const slse = reinterpret_cast<float*>(smem + 2 * G::NAT_BYTES + 2 * G::TRN_BYTES);
-  float* const sdl = slse + BMQ;
+  // two buffers x (Q tile, dO tile, lse[64], delta[64])
+  constexpr int BUF = 2 * G::BYTES + 2 * BMQ * 4;
+  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
   // heavy first: for causal, early key blocks are attended by the most queries
@@ -188,52 +213,94 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
 
   const bool wave_live = wk0 < p.kv_len;
   const int q_begin = CAUSAL ? (k0 / BMQ) * BMQ : 0;
-  // keys of the whole workgroup at or past kv_len: gradients are exactly zero
-  const int n_members = (k0 < p.kv_len) ? p.g : 0;
+  const int nqb = (k0 < p.kv_len && q_begin < p.Sq) ? (p.Sq - q_begin + BMQ - 1) / BMQ : 0;
+  const int nsteps = nqb * p.g;  // (group member, q block), member-major
 
-  for (int member = 0; member < n_members; ++member) {
-    const int h = kvh * p.g + member;
+  TileRegs<T, D> qreg, doreg;
+  float lreg = 0.f;  // threads 0..63 stage lse, 64..127 stage delta
+  TrAddr<T, D> ta;
+  ta.init(lane);
+
+  auto step_coords = [&](int st, int& h, int& qb0) {
+    const int member = st / nqb;
+    h = kvh * p.g + member;
+    qb0 = q_begin + (st - member * nqb) * BMQ;
+  };
+  auto load_step = [&](int st) {
+    int h, qb0;
+    step_coords(st, h, qb0);
     const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
-    const T* Qb = static_cast<const T*>(p.q) + qoff * D;
-    const T* dOb = static_cast<const T*>(p.dout) + qoff * D;
-    for (int qb0 = q_begin; qb0 < p.Sq; qb0 += BMQ) {
-      __syncthreads();
-      stage_tile<T, D>(Qb, qb0, p.Sq, sq, sqt, tid);
-      stage_tile<T, D>(dOb, qb0, p.Sq, sdo, sdot, tid);
-      if (tid < BMQ) {
-        const int q = qb0 + tid;
-        slse[tid] = q < p.Sq ? p.lse[qoff + q] * kLog2e : 0.f;
-        sdl[tid] = q < p.Sq ? p.delta[qoff + q] : 0.f;
-      }
-      __syncthreads();
-      if (!wave_live) continue;
-      if (CAUSAL && qb0 + BMQ - 1 < wk0) continue;  // all these queries precede the wave's keys
+    const uint32_t qbytes = (uint32_t)p.Sq * (uint32_t)G::RB;
+    qreg.load(make_rsrc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, tid);
+    doreg.load(make_rsrc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, tid);
+    if (tid < 2 * BMQ) {
+      const int q = qb0 + (tid & (BMQ - 1));
+      if (q < p.Sq) lreg = tid < BMQ ? p.lse[qoff + q] * kLog2e : p.delta[qoff + q];
+      else lreg = 0.f;
+    }
+  };
+  auto store_step = [&](char* buf) {
+    qreg.store(buf, tid);
+    doreg.store(buf + G::BYTES, tid);
+    if (tid < 2 * BMQ) reinterpret_cast<float*>(buf + 2 * G::BYTES)[tid] = lreg;
+  };
 
+  if (nsteps > 0) {
+    load_step(0);
+    store_step(smem);
+  }
+  __syncthreads();
+
+  for (int st = 0; st < nsteps; ++st) {
+    const char* buf = smem + (st & 1) * BUF;
+    const char* sq = buf;
+    const char* sdo = buf + G::BYTES;
+    const float* slse = reinterpret_cast<const float*>(buf + 2 * G::BYTES);
+    const float* sdl = slse + BMQ;
+    int h_unused, qb0;
+    step_coords(st, h_unused, qb0);
+    const bool has_next = st + 1 < nsteps;
+    if (has_next) load_step(st + 1);
+
+    if (wave_live && !(CAUSAL && qb0 + BMQ - 1 < wk0)) {
       f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f), d0 = (f32x16)(0.f), d1 = (f32x16)(0.f);
-      mfma_rows_x_frags<T, D>(sq, l32, hh, kf, s0, s1);
-      mfma_rows_x_frags<T, D>(sdo, l32, hh, vf, d0, d1);
+      mfma_nat<T, D>(sq, l32, hh, kf, s0, s1);
+      mfma_nat<T, D>(sdo, l32, hh, vf, d0, d1);
 
       // lane = key kkey; tile t register r = query qb0 + 32hh + 16t + r
+      const bool need_mask = !kvalid || (qb0 + BMQ > p.Sq) || (CAUSAL && qb0 < wk0 + 31);
       f32x16 pp0, pp1;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t) {
+        const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
+        const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = 32 * hh + 16 * t + r;
-          const int q = qb0 + qi;
-          const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
-          const float sx = t ? s1[r] : s0[r];
-          const float dp = t ? d1[r] : d0[r];
-          const float pv = ok ? exp2f(sx * p.scale_log2 - slse[qi]) : 0.f;
-          const float ds = pv * (dp - sdl[qi]);
-          if (t) { pp1[r] = pv; s1[r] = ds; } else { pp0[r] = pv; s0[r] = ds; }
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 lv = l4[r4], dl = d4[r4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            const float sx = t ? s1[r] : s0[r];
+            const float dp = t ? d1[r] : d0[r];
+            float pv = __builtin_amdgcn_exp2f(fmaf(sx, p.scale_log2, -lv[e]));
+            if (need_mask) {
+              const int q = qb0 + 32 * hh + 16 * t + r;
+              const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
+              pv = ok ? pv : 0.f;
+            }
+            const float ds = pv * (dp - dl[e]);
+            if (t) { pp1[r] = pv; s1[r] = ds; } else { pp0[r] = pv; s0[r] = ds; }
+          }
         }
+      }
       Frag pfr[PF], dsf[PF];
       pack_frags<T>(pp0, pp1, pfr);
       pack_frags<T>(s0, s1, dsf);
-      mfma_trn_x_frags<T, D>(sdot, l32, hh, pfr, dv);
-      mfma_trn_x_frags<T, D>(sqt, l32, hh, dsf, dk);
+      mfma_trn<T, D>(sdo, lane, ta, pfr, dv);
+      mfma_trn<T, D>(sq, lane, ta, dsf, dk);
     }
+    if (has_next) store_step(smem + ((st + 1) & 1) * BUF);
+    __syncthreads();
   }
 
   if (kkey < p.Sk) {

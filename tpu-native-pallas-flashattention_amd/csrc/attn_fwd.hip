@@ -37,6 +37,8 @@
 #include "pf_kernels.hpp"
 #include "pf_tiles.hpp"
 
+#include <type_traits>
+
 namespace pf {
 
 namespace {
@@ -44,40 +46,75 @@ namespace {
 constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdBN = 64;   // keys per block
 
-template <typename T, int D, bool ROPE>
-struct FwdTiles {
-  static constexpr int ES = sizeof(T);
-  static constexpr int EPC = 16 / ES;         // elements per 16-byte chunk
-  static constexpr int CPR = D / EPC;         // chunks per row
-  static constexpr bool TR = (ES == 2);       // transposing LDS reads for V
-  static constexpr int K_BYTES = kFwdBN * D * ES;
-  static constexpr int VT_PITCH = kFwdBN * ES + 16;
-  static constexpr int V_BYTES = TR ? kFwdBN * D * ES : D * VT_PITCH;
-  static constexpr int K_ITEMS = ROPE ? kFwdBN * CPR / 2 : kFwdBN * CPR;   // per block
-  static constexpr int K_PER_T = (K_ITEMS + 255) / 256;
-  static constexpr int K_CHUNKS = ROPE ? 2 : 1;                             // chunks per item
-  static constexpr int V_ITEMS = TR ? kFwdBN * CPR : 16 * CPR;              // f32: 4-row groups
-  static constexpr int V_PER_T = (V_ITEMS + 255) / 256;
-  static constexpr int V_CHUNKS = TR ? 1 : 4;
-  // 16-byte chunk swizzles (row-dependent XOR keeps each row's chunks in place)
-  __device__ static int kswz(int row) { return row & (CPR >= 16 ? 15 : CPR - 1); }
-  __device__ static int vswz(int row) { return CPR >= 16 ? 4 * (row & 3) : 4 * (row & 1); }
+// Fused-RoPE K staging: each item is a (row, chunk) pair of the first half of
+// the row together with its partner chunk D/2 further, rotated in float32
+// (x*cos + rotate_half(x)*sin, fused_rope.py:43-50, :75-78) before the store.
+template <typename T, int D>
+struct RopeTileRegs {
+  using G = Tile<T, D>;
+  static constexpr int ITEMS = 64 * G::CPR / 2;
+  static constexpr int PER_T = (ITEMS + 255) / 256;
+  u32x4 lo[PER_T], hi[PER_T];
+
+  __device__ inline void load(rsrc_t rs, int row0, int tid) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int c = tid + 256 * u;
+      if (ITEMS % 256 == 0 || c < ITEMS) {
+        const int row = c / (G::CPR / 2), pc = c % (G::CPR / 2);
+        const uint32_t off = (uint32_t)((row0 + row) * D + pc * G::EPC) * G::ES;
+        lo[u] = bufld16(rs, off);
+        hi[u] = bufld16(rs, off + (D / 2) * G::ES);
+      }
+    }
+  }
+  __device__ inline void store(char* tile, int row0, int valid_rows, const float* cosb, const float* sinb,
+                               int tid) const {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int c = tid + 256 * u;
+      if (ITEMS % 256 == 0 || c < ITEMS) {
+        const int row = c / (G::CPR / 2), pc = c % (G::CPR / 2);
+        u32x4 lo_out = {0u, 0u, 0u, 0u}, hi_out = {0u, 0u, 0u, 0u};
+        if (row0 + row < valid_rows) {  // tables are [Sk, D]: read only for valid keys
+          float a[G::EPC], b[G::EPC], ra[G::EPC], rb[G::EPC];
+          chunk_to_f32<T>(lo[u], a);
+          chunk_to_f32<T>(hi[u], b);
+          const float* cs = cosb + (int64_t)(row0 + row) * D + pc * G::EPC;
+          const float* sn = sinb + (int64_t)(row0 + row) * D + pc * G::EPC;
+#pragma unroll
+          for (int e = 0; e < G::EPC; ++e) {
+            ra[e] = a[e] * cs[e] - b[e] * sn[e];
+            rb[e] = b[e] * cs[D / 2 + e] + a[e] * sn[D / 2 + e];
+          }
+          lo_out = f32_to_chunk<T>(ra);
+          hi_out = f32_to_chunk<T>(rb);
+        }
+        char* dst = tile + row * G::RB;
+        const int sw = tile_swz<G::CPR>(row);
+        sts16(dst + 16 * (pc ^ sw), lo_out);
+        sts16(dst + 16 * ((pc + G::CPR / 2) ^ sw), hi_out);
+      }
+    }
+  }
 };
 
 template <typename T, int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_attn_fwd_kernel(FwdParams p) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
-  using G = FwdTiles<T, D, ROPE>;
+  using G = Tile<T, D>;
   constexpr int BM = kFwdBM, BN = kFwdBN;
   constexpr int HALF = D / 2;
-  constexpr int ES = G::ES, EPC = G::EPC, CPR = G::CPR;
+  constexpr int ES = G::ES, EPC = G::EPC;
   constexpr int FPC = frags_per_chunk<T>();
   constexpr int QF = HALF / MF::kK;  // Q fragments per lane
   constexpr int NDT = D / 32;        // 32-row tiles of O^T
   constexpr int PF = 32 / MF::kK;    // P fragments per lane per block
+  static_assert(BN == 64, "one K/V block is one 64-row tile");
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * (G::K_BYTES + G::V_BYTES)];
+  // two buffers x (K tile, V tile)
+  __shared__ __attribute__((aligned(16))) char smem[4 * G::BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -146,96 +183,21 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       for (int f = 0; f < FPC; ++f) qf[c * FPC + f] = chunk_frag<T>(qc[c], f);
   }
 
-  // ---- staging registers for one K/V block ---------------------------------
-  u32x4 kreg[G::K_PER_T][G::K_CHUNKS];
-  u32x4 vreg[G::V_PER_T][G::V_CHUNKS];
-
-  // K/V of this (batch, kv head): rows at or past kv_len lie outside the
-  // resource and load as zeros (never read from memory).
+  // ---- staging: K/V rows at or past kv_len lie outside the buffer resources
+  // and load as zeros (never read from memory).
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
   const rsrc_t krs = make_rsrc(Kb, kv_bytes);
   const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
-
+  typename std::conditional<ROPE, RopeTileRegs<T, D>, TileRegs<T, D>>::type kreg;
+  TileRegs<T, D> vreg;
   auto load_block = [&](int kv0) {
-#pragma unroll
-    for (int u = 0; u < G::K_PER_T; ++u) {
-      const int c = tid + 256 * u;
-      if (G::K_ITEMS % 256 == 0 || c < G::K_ITEMS) {
-        const int r = ROPE ? c / (CPR / 2) : c / CPR;
-        const int cc = ROPE ? c % (CPR / 2) : c % CPR;
-        const uint32_t off = (uint32_t)((kv0 + r) * D + cc * EPC) * ES;
-        kreg[u][0] = bufld16(krs, off);
-        if constexpr (ROPE) kreg[u][G::K_CHUNKS - 1] = bufld16(krs, off + HALF * ES);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < G::V_PER_T; ++u) {
-      const int c = tid + 256 * u;
-      if (G::V_ITEMS % 256 == 0 || c < G::V_ITEMS) {
-        if constexpr (G::TR) {
-          const int r = c / CPR, cc = c % CPR;
-          vreg[u][0] = bufld16(vrs, (uint32_t)((kv0 + r) * D + cc * EPC) * ES);
-        } else {
-          const int kg = c & 15, dc = c >> 4;
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            vreg[u][r] = bufld16(vrs, (uint32_t)((kv0 + 4 * kg + r) * D + dc * EPC) * ES);
-        }
-      }
-    }
+    kreg.load(krs, kv0, tid);
+    vreg.load(vrs, kv0, tid);
   };
-
   auto store_block = [&](int kv0, char* sk, char* sv) {
-#pragma unroll
-    for (int u = 0; u < G::K_PER_T; ++u) {
-      const int c = tid + 256 * u;
-      if (G::K_ITEMS % 256 == 0 || c < G::K_ITEMS) {
-        if constexpr (ROPE) {
-          const int r = c / (CPR / 2), pc = c % (CPR / 2);
-          const int key = kv0 + r;
-          u32x4 lo_out = {0u, 0u, 0u, 0u}, hi_out = {0u, 0u, 0u, 0u};
-          if (key < p.kv_len) {  // tables are [Sk, D]: only read for valid keys
-            float lo[EPC], hi[EPC], rlo[EPC], rhi[EPC];
-            chunk_to_f32<T>(kreg[u][0], lo);
-            chunk_to_f32<T>(kreg[u][1], hi);
-            const float* cs = p.k_cos + (int64_t)key * D + pc * EPC;
-            const float* sn = p.k_sin + (int64_t)key * D + pc * EPC;
-#pragma unroll
-            for (int e = 0; e < EPC; ++e) {
-              rlo[e] = lo[e] * cs[e] - hi[e] * sn[e];
-              rhi[e] = hi[e] * cs[HALF + e] + lo[e] * sn[HALF + e];
-            }
-            lo_out = f32_to_chunk<T>(rlo);
-            hi_out = f32_to_chunk<T>(rhi);
-          }
-          const int pr = perm_row(r);
-          char* dst = sk + pr * (D * ES);
-          sts16(dst + 16 * (pc ^ G::kswz(pr)), lo_out);
-          sts16(dst + 16 * ((pc + CPR / 2) ^ G::kswz(pr)), hi_out);
-        } else {
-          const int r = c / CPR, cc = c % CPR;
-          const int pr = perm_row(r);
-          sts16(sk + pr * (D * ES) + 16 * (cc ^ G::kswz(pr)), kreg[u][0]);
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < G::V_PER_T; ++u) {
-      const int c = tid + 256 * u;
-      if (G::V_ITEMS % 256 == 0 || c < G::V_ITEMS) {
-        if constexpr (G::TR) {
-          const int r = c / CPR, cc = c % CPR;
-          sts16(sv + r * (D * ES) + 16 * (cc ^ G::vswz(r)), vreg[u][0]);
-        } else {
-          const int kg = c & 15, dc = c >> 4;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const u32x4 o4 = {vreg[u][0][e], vreg[u][1][e], vreg[u][2][e], vreg[u][3][e]};
-            sts16(sv + (dc * 4 + e) * G::VT_PITCH + kg * 16, o4);
-          }
-        }
-      }
-    }
+    if constexpr (ROPE) kreg.store(sk, kv0, p.kv_len, p.k_cos, p.k_sin, tid);
+    else kreg.store(sk, tid);
+    vreg.store(sv, tid);
   };
 
   float m_run = kNegInf;  // running max, log2 domain (identical in both halves)
@@ -249,29 +211,19 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const int nblk = (kv_end + BN - 1) / BN;
   const float c2 = fabsf(p.scale_log2);
 
-  // Per-lane byte offsets of the V^T fragment reads (16-bit types). Lane
-  // (group gq = lane/16, j = lane%16) points at V[32(gq/2) + 8c + 4r + j/4]
-  // [32dt + 16(gq%2) + 4(j%4)]; the row swizzle only depends on row%4 =
-  // (j/4)%4, so the per-dt chunk offsets are lane constants.
-  const int tr_g = lane >> 4, tr_j = lane & 15;
-  const int tr_row0 = 32 * (tr_g >> 1) + (tr_j >> 2);
-  const int tr_col0 = 16 * (tr_g & 1) + 4 * (tr_j & 3);
-  const int tr_sw = G::TR ? G::vswz(tr_row0) : 0;
-  const int tr_base = tr_row0 * (D * ES) + 16 * (tr_col0 >> 3) + 2 * (tr_col0 & 7);
-  int tr_dt[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) tr_dt[dt] = tr_base + 16 * ((4 * dt) ^ tr_sw);
+  TrAddr<T, D> vta;
+  vta.init(lane);
 
   if (nblk > 0) {
     load_block(0);
-    store_block(0, smem, smem + G::K_BYTES);
+    store_block(0, smem, smem + G::BYTES);
   }
   __syncthreads();
 
   for (int j = 0; j < nblk; ++j) {
     const int kv0 = j * BN;
-    char* const sk = smem + (j & 1) * (G::K_BYTES + G::V_BYTES);
-    char* const sv = sk + G::K_BYTES;
+    char* const sk = smem + (j & 1) * (2 * G::BYTES);
+    char* const sv = sk + G::BYTES;
     const bool has_next = j + 1 < nblk;
     if (has_next) load_block(kv0 + BN);
 
@@ -281,22 +233,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       f32x16 s[2];
       s[0] = (f32x16)(0.f);
       s[1] = (f32x16)(0.f);
-      {
-        const char* kr0 = sk + l32 * (D * ES);
-        const char* kr1 = sk + (32 + l32) * (D * ES);
-        const int sw0 = G::kswz(l32), sw1 = G::kswz(32 + l32);
-#pragma unroll
-        for (int c = 0; c < HALF / EPC; ++c) {
-          const int ch = hh * (CPR / 2) + c;
-          const u32x4 a0 = lds16(kr0 + 16 * (ch ^ sw0));
-          const u32x4 a1 = lds16(kr1 + 16 * (ch ^ sw1));
-#pragma unroll
-          for (int f = 0; f < FPC; ++f) {
-            s[0] = MF::run(chunk_frag<T>(a0, f), qf[c * FPC + f], s[0]);
-            s[1] = MF::run(chunk_frag<T>(a1, f), qf[c * FPC + f], s[1]);
-          }
-        }
-      }
+      mfma_nat<T, D>(sk, l32, hh, qf, s[0], s[1]);
 
       // ---- online softmax (lane owns query qrow; keys kv0 + 32hh + 16t + r)
       // c2 = |scale| * log2(e) >= 0. The running reference m_run only moves
@@ -360,39 +297,12 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       pack_frags<T>(s[0], s[1], pfr);
 
       // ---- O^T += V^T . P^T -------------------------------------------------
-      if constexpr (G::TR) {
-        typedef short v4i16 __attribute__((ext_vector_type(4)));
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            v4i16 part[2];
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-              const char* a = sv + tr_dt[dt] + (8 * c + 4 * r) * (D * ES);
-              part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (__attribute__((address_space(3))) v4i16*)(a));
-            }
-            const Frag af = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[dt] = MF::run(af, pfr[c], acc[dt]);
-          }
-      } else {
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const char* vr = sv + (32 * dt + l32) * G::VT_PITCH + hh * 32 * ES;
-#pragma unroll
-          for (int c = 0; c < 32 * ES / 16; ++c) {
-            const u32x4 a = lds16(vr + c * 16);
-#pragma unroll
-            for (int f = 0; f < FPC; ++f) acc[dt] = MF::run(chunk_frag<T>(a, f), pfr[c * FPC + f], acc[dt]);
-          }
-        }
-      }
+      mfma_trn<T, D>(sv, lane, vta, pfr, acc);
     }
 
     if (has_next) {
-      char* const nk = smem + ((j + 1) & 1) * (G::K_BYTES + G::V_BYTES);
-      store_block(kv0 + BN, nk, nk + G::K_BYTES);
+      char* const nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
+      store_block(kv0 + BN, nk, nk + G::BYTES);
     }
     __syncthreads();
   }

@@ -1,113 +1,157 @@
-// LDS tile staging shared by the prefill-shaped kernels.
+// LDS tiles shared by the prefill-shaped kernels (forward, dQ, dK/dV).
 //
-// A "64-row tile" is rows [row0, row0 + 64) of a row-major [rows, D] matrix.
-// It can be staged two ways:
-//  * natural, row-permuted (pitch D*sizeof(T) + 16 bytes): tile row r lands
-//    at LDS row perm_row(r), so that a 32x32 MFMA whose A operand reads LDS
-//    rows 32t + (lane % 32) produces, in lane half hh / accumulator register
-//    reg, the tile row 32hh + 16t + reg;
-//  * transposed (pitch 64*sizeof(T) + 16 bytes): LDS row d holds column d of
-//    the tile with the 64 tile rows contiguous, which is the layout an MFMA
-//    operand needs when the product contracts over the tile rows.
-// Rows at or past `limit` are written as zeros and never read from memory.
+// A tile is 64 consecutive rows of a row-major [rows, D] matrix of T, staged
+// in LDS unpadded (row pitch D*sizeof(T)), with each row's 16-byte chunks
+// XOR-swizzled by tile_swz(row). Two MFMA operand reads come out of the same
+// copy:
+//  * "natural" A operand (contraction over D): MFMA row R = lane%32 of 32-row
+//    tile t reads tile row mfma_src_row(R, t), so that in the result lane half
+//    hh's accumulator register reg holds tile row 32hh + 16t + reg -- exactly
+//    the reduction slots that the next MFMA's B operand needs from that lane;
+//  * "transposed" A operand (contraction over the 64 tile rows): for 16-bit T
+//    the gfx950 transposing LDS load ds_read_b64_tr_b16 (within each 16-lane
+//    group, lane i receives element [4t + i/4][i%4] of the 16 x 4 block the
+//    group addressed; lane j pointing at row k0 + j/4, column d0 + 4(j%4)
+//    hands lane i the values [k0 + t][d0 + i]); for float32, scalar reads.
+// The swizzle makes both read kinds and the staging writes conflict-free:
+// the 16 lanes of a natural read hit 16 distinct chunks, and a transposed read
+// (4 consecutive rows x 4 consecutive chunks) hits 16 distinct chunks.
+// Rows at or past a limit are loaded as zeros by the buffer resource.
 #pragma once
 
 #include "pf_common.hpp"
 
 namespace pf {
 
-__device__ inline int perm_row(int r) {
-  return ((r >> 4) & 1) * 32 + ((r >> 2) & 3) * 8 + (r >> 5) * 4 + (r & 3);
+__device__ inline int mfma_src_row(int R, int t) {
+  return 32 * ((R >> 2) & 1) + 16 * t + 4 * (R >> 3) + (R & 3);
+}
+
+template <int CPR>
+__device__ inline int tile_swz(int row) {
+  if constexpr (CPR >= 16) {
+    return ((row & 3) << 2) | (((row >> 2) & 1) << 1) | ((row >> 5) & 1);
+  } else {
+    return (((row >> 1) & 1) << 2) | (((row >> 2) & 1) << 1) | ((row >> 5) & 1);
+  }
 }
 
 template <typename T, int D>
-struct TileGeom {
+struct Tile {
   static constexpr int ES = sizeof(T);
-  static constexpr int EPC = 16 / ES;           // elements per 16-byte chunk
-  static constexpr int NDC = D / EPC;           // chunks per row
-  static constexpr int NAT_PITCH = D * ES + 16; // natural layout row pitch
-  static constexpr int TRN_PITCH = 64 * ES + 16;
-  static constexpr int NAT_BYTES = 64 * NAT_PITCH;
-  static constexpr int TRN_BYTES = D * TRN_PITCH;
-  static constexpr int ITEMS = 16 * NDC;        // (4-row group, chunk) items
+  static constexpr int EPC = 16 / ES;      // elements per 16-byte chunk
+  static constexpr int CPR = D / EPC;      // chunks per row
+  static constexpr int RB = D * ES;        // row bytes
+  static constexpr int BYTES = 64 * RB;
+  static constexpr int PER_T = 64 * CPR / 256;  // chunks staged per thread (256 threads)
+  static constexpr bool TR = (ES == 2);
 };
 
-// Stage a 64-row tile with all 256 threads of a workgroup. `src` points at
-// row 0 of the matrix (row stride D). Writes the natural (permuted) copy to
-// `nat` and/or the transposed copy to `trn` (either may be null).
+// Register staging of one tile: coalesced 16-byte buffer loads (a wave reads
+// whole rows), then swizzled LDS stores.
 template <typename T, int D>
-__device__ inline void stage_tile(const T* src, int row0, int limit, char* nat, char* trn, int tid) {
-  using G = TileGeom<T, D>;
+struct TileRegs {
+  using G = Tile<T, D>;
+  u32x4 r[G::PER_T];
+
+  __device__ inline void load(rsrc_t rs, int row0, int tid) {
 #pragma unroll
-  for (int u = 0; u < (G::ITEMS + 255) / 256; ++u) {
-    const int c = tid + 256 * u;
-    if (G::ITEMS % 256 != 0 && c >= G::ITEMS) break;
-    const int kg = c & 15, dc = c >> 4;
-    u32x4 ch[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + 4 * kg + r;
-      ch[r] = (row < limit) ? ldg16(src + (int64_t)row * D + dc * G::EPC) : (u32x4){0u, 0u, 0u, 0u};
-    }
-    if (nat != nullptr) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sts16(nat + perm_row(4 * kg + r) * G::NAT_PITCH + dc * 16, ch[r]);
-    }
-    if (trn != nullptr) {
-      if constexpr (G::ES == 4) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const u32x4 o4 = {ch[0][e], ch[1][e], ch[2][e], ch[3][e]};
-          sts16(trn + (dc * 4 + e) * G::TRN_PITCH + kg * 16, o4);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int wd = e >> 1, sh = (e & 1) * 16;
-          const uint32_t v0 = (ch[0][wd] >> sh) & 0xffffu, v1 = (ch[1][wd] >> sh) & 0xffffu;
-          const uint32_t v2 = (ch[2][wd] >> sh) & 0xffffu, v3 = (ch[3][wd] >> sh) & 0xffffu;
-          const u32x2 o2 = {v0 | (v1 << 16), v2 | (v3 << 16)};
-          *reinterpret_cast<u32x2*>(trn + (dc * 8 + e) * G::TRN_PITCH + kg * 8) = o2;
-        }
-      }
+    for (int u = 0; u < G::PER_T; ++u) {
+      const int c = tid + 256 * u;
+      const int row = c / G::CPR, cc = c % G::CPR;
+      r[u] = bufld16(rs, (uint32_t)((row0 + row) * D + cc * G::EPC) * G::ES);
     }
   }
-}
-
-// Load a lane's operand fragments for row `row` (lane half hh owns columns
-// [hh*D/2, (hh+1)*D/2)); zeros when the row is out of range.
-template <typename T, int D>
-__device__ inline void load_row_frags(const T* src, int row, bool valid, int hh,
-                                      typename Mfma32<T>::Frag* out) {
-  constexpr int EPC = 16 / (int)sizeof(T);
-  constexpr int FPC = frags_per_chunk<T>();
-  const T* r = src + (int64_t)row * D + hh * (D / 2);
+  __device__ inline void store(char* tile, int tid) const {
 #pragma unroll
-  for (int c = 0; c < D / 2 / EPC; ++c) {
-    const u32x4 ch = valid ? ldg16(r + c * EPC) : (u32x4){0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int f = 0; f < FPC; ++f) out[c * FPC + f] = chunk_frag<T>(ch, f);
+    for (int u = 0; u < G::PER_T; ++u) {
+      const int c = tid + 256 * u;
+      const int row = c / G::CPR, cc = c % G::CPR;
+      sts16(tile + row * G::RB + 16 * (cc ^ tile_swz<G::CPR>(row)), r[u]);
+    }
   }
-}
+};
 
-// acc(32x32 tiles t=0,1) += A rows from a natural-permuted LDS tile x B frags
-// (contraction over D): the "S^T = K Q^T" step.
+// Natural A operand: s0/s1 (32x32 tiles t = 0, 1) += tile rows x B fragments,
+// contracting over D (lane half hh owns columns [hh*D/2, (hh+1)*D/2)).
 template <typename T, int D>
-__device__ inline void mfma_rows_x_frags(const char* nat, int l32, int hh,
-                                         const typename Mfma32<T>::Frag* bf, f32x16& s0, f32x16& s1) {
+__device__ inline void mfma_nat(const char* tile, int l32, int hh, const typename Mfma32<T>::Frag* bf,
+                                f32x16& s0, f32x16& s1) {
   using MF = Mfma32<T>;
-  using G = TileGeom<T, D>;
+  using G = Tile<T, D>;
   constexpr int FPC = frags_per_chunk<T>();
-  const char* r0 = nat + l32 * G::NAT_PITCH + hh * (D / 2) * G::ES;
-  const char* r1 = nat + (32 + l32) * G::NAT_PITCH + hh * (D / 2) * G::ES;
+  const int r0 = mfma_src_row(l32, 0), r1 = mfma_src_row(l32, 1);
+  const char* b0 = tile + r0 * G::RB;
+  const char* b1 = tile + r1 * G::RB;
+  const int sw0 = tile_swz<G::CPR>(r0), sw1 = tile_swz<G::CPR>(r1);
 #pragma unroll
-  for (int c = 0; c < D / 2 / G::EPC; ++c) {
-    const u32x4 a0 = lds16(r0 + c * 16);
-    const u32x4 a1 = lds16(r1 + c * 16);
+  for (int c = 0; c < G::CPR / 2; ++c) {
+    const int ch = hh * (G::CPR / 2) + c;
+    const u32x4 a0 = lds16(b0 + 16 * (ch ^ sw0));
+    const u32x4 a1 = lds16(b1 + 16 * (ch ^ sw1));
 #pragma unroll
     for (int f = 0; f < FPC; ++f) {
       s0 = MF::run(chunk_frag<T>(a0, f), bf[c * FPC + f], s0);
       s1 = MF::run(chunk_frag<T>(a1, f), bf[c * FPC + f], s1);
+    }
+  }
+}
+
+// Per-lane byte offsets for the transposed reads of a tile (16-bit types):
+// off[dt][r] + (8c + 4r) * RB addresses the 8 bytes lane `lane` contributes to
+// step c, half r of the 32-column block dt.
+template <typename T, int D>
+struct TrAddr {
+  using G = Tile<T, D>;
+  int off[D / 32][2];
+  __device__ inline void init(int lane) {
+    const int g = lane >> 4, j = lane & 15, hh = lane >> 5;
+    const int a = j >> 2;                          // row within the 4-row group
+    const int x = 2 * (g & 1) + ((j >> 1) & 1);    // chunk within the 4-chunk group
+    const int q = G::CPR >= 16 ? 4 * a : 4 * (a >> 1);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        off[dt][r] = (32 * hh + a) * G::RB + 8 * (j & 1) + 16 * (((4 * dt) ^ q) + (x ^ (2 * r + hh)));
+  }
+};
+
+// Transposed A operand: acc[dt] += tile^T (rows = D columns of the tile,
+// reduction over the tile's 64 rows) x B fragments. Lane half hh's B slots
+// for step c are tile rows 32hh + 8c + [0, 8) (16-bit) or 32hh + s (f32).
+template <typename T, int D>
+__device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& ta,
+                                const typename Mfma32<T>::Frag* bf, f32x16* acc) {
+  using MF = Mfma32<T>;
+  using G = Tile<T, D>;
+  using Frag = typename MF::Frag;
+  if constexpr (G::TR) {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v4i16 part[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+          part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)(tile + ta.off[dt][r] + (8 * c + 4 * r) * G::RB));
+        const Frag af = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        acc[dt] = MF::run(af, bf[c], acc[dt]);
+      }
+  } else {
+    const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      const int d = 32 * dt + l32;
+#pragma unroll
+      for (int s = 0; s < 32; ++s) {
+        const int row = 32 * hh + s;
+        const float a = *reinterpret_cast<const float*>(
+            tile + row * G::RB + 16 * ((d >> 2) ^ tile_swz<G::CPR>(row)) + 4 * (d & 3));
+        acc[dt] = MF::run(a, bf[s], acc[dt]);
+      }
     }
   }
 }
@@ -134,23 +178,19 @@ __device__ inline void pack_frags(const f32x16& s0, const f32x16& s1, typename M
   }
 }
 
-// acc[dt] += A rows of a transposed LDS tile (row 32dt + l32, this lane half's
-// 32 contiguous tile rows) x packed B frags: the "O^T += V^T P^T" step.
+// Load a lane's operand fragments for row `row` (lane half hh owns columns
+// [hh*D/2, (hh+1)*D/2)); zeros when the row is out of range.
 template <typename T, int D>
-__device__ inline void mfma_trn_x_frags(const char* trn, int l32, int hh,
-                                        const typename Mfma32<T>::Frag* bf, f32x16* acc) {
-  using MF = Mfma32<T>;
-  using G = TileGeom<T, D>;
+__device__ inline void load_row_frags(const T* src, int row, bool valid, int hh,
+                                      typename Mfma32<T>::Frag* out) {
+  constexpr int EPC = 16 / (int)sizeof(T);
   constexpr int FPC = frags_per_chunk<T>();
+  const T* r = src + (int64_t)row * D + hh * (D / 2);
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
-    const char* r = trn + (32 * dt + l32) * G::TRN_PITCH + hh * 32 * G::ES;
+  for (int c = 0; c < D / 2 / EPC; ++c) {
+    const u32x4 ch = valid ? ldg16(r + c * EPC) : (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int c = 0; c < 32 * G::ES / 16; ++c) {
-      const u32x4 a = lds16(r + c * 16);
-#pragma unroll
-      for (int f = 0; f < FPC; ++f) acc[dt] = MF::run(chunk_frag<T>(a, f), bf[c * FPC + f], acc[dt]);
-    }
+    for (int f = 0; f < FPC; ++f) out[c * FPC + f] = chunk_frag<T>(ch, f);
   }
 }
 
