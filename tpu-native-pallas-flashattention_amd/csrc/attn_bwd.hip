@@ -1,374 +1,43 @@
-// Backward attention for gfx950: delta preprocess, dQ kernel, dK/dV kernel.
-//
-// Replaces `_flash_attention_bwd_call` (flash_attention.py:354-442):
-//   delta_i = sum_d o_id * do_id            (XLA op, :363-365) -> delta kernel
-//   flash_attention_bwd_dq  pallas_call     (:379-398, kernel :276-311)
-//   flash_attention_bwd_dkv pallas_call     (:403-431, kernel :314-351)
-//   GQA group sum of per-head dK/dV         (:433-436)
-// Both gradient kernels recompute p = exp(s - lse) from the forward LSE
-// (_bwd_common, :245-273) and apply the same masks: k < kv_len, q < Sq and
-// (causal) q >= k. The dK/dV kernel loops over the query heads of its GQA
-// group and accumulates dK/dV in registers, so the group sum happens in
-// float32 inside the kernel with one cast at the end -- the reference's
-// per-head float32 [B, Hq, Sk, D] temporaries and the separate sum pass do
-// not exist here.
-//
-// Both kernels use the forward's pipeline: 64-row LDS tiles staged with
-// bounds-checked buffer loads, double-buffered with one barrier per step, and
-// every transposed operand read from the single natural copy with the
-// transposing LDS load (pf_tiles.hpp).
-//  dQ (workgroup = 128 query rows, 4 waves x 32 rows; loop over 64-key blocks):
-//    S^T = K Q^T, dP^T = V dO^T  (K, V tiles; Q, dO in registers)
-//    dS^T = P^T (dP^T - delta);  dQ^T += K^T dS^T  (K^T from the K tile)
-//  dK/dV (workgroup = 128 keys, 4 waves x 32 keys; loop over the group's
-//  heads x 64-row query blocks):
-//    S = Q K^T, dP = dO V^T  (Q, dO tiles; K, V in registers)
-//    dS = P (dP - delta);  dV^T += dO^T P,  dK^T += Q^T dS  (from the same tiles)
-#include "pf_common.hpp"
-#include "pf_kernels.hpp"
-#include "pf_tiles.hpp"
+// Backward launch entry points (kernels in attn_bwd.hpp). The 16-bit delta and
+// dQ instantiations live in this translation unit; the 16-bit dK/dV kernel is
+// built in attn_bwd_dkv16.hip and the float32 ones in attn_bwd_f32.hip, each
+// with its own code-generation flags (see the Makefile).
+#include "attn_bwd.hpp"
 
 namespace pf {
 
-namespace {
+hipError_t launch_bwd_delta_f32(const BwdParams& p, int head_dim, hipStream_t stream);
+hipError_t launch_bwd_dq_f32(const BwdParams& p, int head_dim, bool causal, hipStream_t stream);
+hipError_t launch_bwd_dkv_f32(const BwdParams& p, int head_dim, bool causal, hipStream_t stream);
+hipError_t launch_bwd_dkv16(const BwdParams& p, int dtype, int head_dim, bool causal, hipStream_t stream);
 
-// ---------------------------------------------------------------------------
-// delta[b, h, i] = sum_d f32(o[b,h,i,d]) * f32(do[b,h,i,d])
-// ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ __launch_bounds__(256) void pf_attn_bwd_delta_kernel(BwdParams p) {
-  constexpr int EPC = 16 / (int)sizeof(T);
-  constexpr int LPR = D / EPC;       // lanes per row
-  constexpr int RPB = 256 / LPR;     // rows per workgroup
-  const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
-  const int sub = threadIdx.x % LPR;
-  float acc = 0.f;
-  if (row < rows) {
-    float a[EPC], c[EPC];
-    chunk_to_f32<T>(ldg16(static_cast<const T*>(p.o) + row * D + sub * EPC), a);
-    chunk_to_f32<T>(ldg16(static_cast<const T*>(p.dout) + row * D + sub * EPC), c);
-#pragma unroll
-    for (int e = 0; e < EPC; ++e) acc += a[e] * c[e];
-  }
-#pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-  if (row < rows && sub == 0) p.delta[row] = acc;
-}
-
-// ---------------------------------------------------------------------------
-// dQ
-// ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2)
-void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
-  using MF = Mfma32<T>;
-  using Frag = typename MF::Frag;
-  using G = Tile<T, D>;
-  constexpr int BM = 128, BN = 64;
-  constexpr int QF = (D / 2) / MF::kK;
-  constexpr int NDT = D / 32;
-  constexpr int PF = 32 / MF::kK;
-
-  // two buffers x (K tile, V tile)
-  __shared__ __attribute__((aligned(16))) char smem[4 * G::BYTES];
-
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
-  const int w = xcd_remap(blockIdx.x, n_work, p.g);
-  const int member = w % p.g;
-  int rest = w / p.g;
-  const int kvh = rest % p.Hkv;
-  rest /= p.Hkv;
-  const int b = rest % p.B;
-  const int qblk = n_qblk - 1 - rest / p.B;
-  const int h = kvh * p.g + member;
-
-  const int q0 = qblk * BM;
-  const int wq0 = q0 + 32 * wv;
-  const int qrow = wq0 + l32;
-  const bool qvalid = qrow < p.Sq;
-  const int wq_last = min(wq0 + 31, p.Sq - 1);
-
-  const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
-  const T* Qb = static_cast<const T*>(p.q) + qoff * D;
-  const T* dOb = static_cast<const T*>(p.dout) + qoff * D;
-  const T* Kb = static_cast<const T*>(p.k) + (int64_t)(b * p.Hkv + kvh) * p.Sk * D;
-  const T* Vb = static_cast<const T*>(p.v) + (int64_t)(b * p.Hkv + kvh) * p.Sk * D;
-
-  Frag qf[QF], dof[QF];
-  load_row_frags<T, D>(Qb, qrow, qvalid, hh, qf);
-  load_row_frags<T, D>(dOb, qrow, qvalid, hh, dof);
-  const float lse2 = qvalid ? p.lse[qoff + qrow] * kLog2e : 0.f;
-  const float dlt = qvalid ? p.delta[qoff + qrow] : 0.f;
-
-  f32x16 acc[NDT];
-#pragma unroll
-  for (int i = 0; i < NDT; ++i) acc[i] = (f32x16)(0.f);
-
-  const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)G::RB;
-  const rsrc_t krs = make_rsrc(Kb, kv_bytes);
-  const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
-  TileRegs<T, D> kreg, vreg;
-  TrAddr<T, D> kta;
-  kta.init(lane);
-
-  int kv_end = p.kv_len;
-  if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + BM, p.Sq));
-  const int nblk = (kv_end + BN - 1) / BN;
-
-  if (nblk > 0) {
-    kreg.load(krs, 0, tid);
-    vreg.load(vrs, 0, tid);
-    kreg.store(smem, tid);
-    vreg.store(smem + G::BYTES, tid);
-  }
-  __syncthreads();
-
-  for (int j = 0; j < nblk; ++j) {
-    const int kv0 = j * BN;
-    const char* sk = smem + (j & 1) * (2 * G::BYTES);
-    const char* sv = sk + G::BYTES;
-    const bool has_next = j + 1 < nblk;
-    if (has_next) {
-      kreg.load(krs, kv0 + BN, tid);
-      vreg.load(vrs, kv0 + BN, tid);
-    }
-    if (wq0 < p.Sq && !(CAUSAL && kv0 > wq_last)) {
-      f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f), d0 = (f32x16)(0.f), d1 = (f32x16)(0.f);
-      mfma_nat<T, D>(sk, l32, hh, qf, s0, s1);
-      mfma_nat<T, D>(sv, l32, hh, dof, d0, d1);
-
-      // keys kv0 + 32hh + 16t + r, query qrow
-      const bool need_mask = !qvalid || (kv0 + BN > p.kv_len) || (CAUSAL && kv0 + BN - 1 > wq0);
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float sx = t ? s1[r] : s0[r];
-          const float dp = t ? d1[r] : d0[r];
-          float pv = __builtin_amdgcn_exp2f(fmaf(sx, p.scale_log2, -lse2));
-          if (need_mask) {
-            const int key = kv0 + 32 * hh + 16 * t + r;
-            const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
-            pv = ok ? pv : 0.f;
-          }
-          const float ds = pv * (dp - dlt);
-          if (t) s1[r] = ds; else s0[r] = ds;
-        }
-      Frag dsf[PF];
-      pack_frags<T>(s0, s1, dsf);
-      mfma_trn<T, D>(sk, lane, kta, dsf, acc);
-    }
-    if (has_next) {
-      char* nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
-      kreg.store(nk, tid);
-      vreg.store(nk + G::BYTES, tid);
-    }
-    __syncthreads();
-  }
-
-  if (qvalid) store_acc_row<T, D>(static_cast<T*>(p.dq) + (qoff + qrow) * D, acc, p.sm_scale, hh);
-}
-
-// ---------------------------------------------------------------------------
-// dK / dV (group-summed)
-// ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, int n_kblk) {
-  using MF = Mfma32<T>;
-  using Frag = typename MF::Frag;
-  using G = Tile<T, D>;
-  constexpr int BNK = 128, BMQ = 64;
-  constexpr int KF = (D / 2) / MF::kK;
-  constexpr int NDT = D / 32;
-  constexpr int PF = 32 / MF::kK;
-
-  // two buffers x (Q tile, dO tile, lse[64], delta[64])
-  constexpr int BUF = 2 * G::BYTES + 2 * BMQ * 4;
-  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
-
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
-  // heavy first: for causal, early key blocks are attended by the most queries
-  const int w = blockIdx.x;
-  const int kblk = w / (p.B * p.Hkv);
-  const int bk = w % (p.B * p.Hkv);
-  const int b = bk / p.Hkv, kvh = bk % p.Hkv;
-
-  const int k0 = kblk * BNK;
-  const int wk0 = k0 + 32 * wv;
-  const int kkey = wk0 + l32;
-  const bool kvalid = kkey < p.kv_len;
-
-  const int64_t koff = (int64_t)(b * p.Hkv + kvh) * p.Sk;
-  Frag kf[KF], vf[KF];
-  load_row_frags<T, D>(static_cast<const T*>(p.k) + koff * D, kkey, kvalid, hh, kf);
-  load_row_frags<T, D>(static_cast<const T*>(p.v) + koff * D, kkey, kvalid, hh, vf);
-
-  f32x16 dk[NDT], dv[NDT];
-#pragma unroll
-  for (int i = 0; i < NDT; ++i) {
-    dk[i] = (f32x16)(0.f);
-    dv[i] = (f32x16)(0.f);
-  }
-
-  const bool wave_live = wk0 < p.kv_len;
-  const int q_begin = CAUSAL ? (k0 / BMQ) * BMQ : 0;
-  const int nqb = (k0 < p.kv_len && q_begin < p.Sq) ? (p.Sq - q_begin + BMQ - 1) / BMQ : 0;
-  const int nsteps = nqb * p.g;  // (group member, q block), member-major
-
-  TileRegs<T, D> qreg, doreg;
-  float lreg = 0.f;  // threads 0..63 stage lse, 64..127 stage delta
-  TrAddr<T, D> ta;
-  ta.init(lane);
-
-  auto step_coords = [&](int st, int& h, int& qb0) {
-    const int member = st / nqb;
-    h = kvh * p.g + member;
-    qb0 = q_begin + (st - member * nqb) * BMQ;
-  };
-  auto load_step = [&](int st) {
-    int h, qb0;
-    step_coords(st, h, qb0);
-    const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
-    const uint32_t qbytes = (uint32_t)p.Sq * (uint32_t)G::RB;
-    qreg.load(make_rsrc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, tid);
-    doreg.load(make_rsrc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, tid);
-    if (tid < 2 * BMQ) {
-      const int q = qb0 + (tid & (BMQ - 1));
-      if (q < p.Sq) lreg = tid < BMQ ? p.lse[qoff + q] * kLog2e : p.delta[qoff + q];
-      else lreg = 0.f;
-    }
-  };
-  auto store_step = [&](char* buf) {
-    qreg.store(buf, tid);
-    doreg.store(buf + G::BYTES, tid);
-    if (tid < 2 * BMQ) reinterpret_cast<float*>(buf + 2 * G::BYTES)[tid] = lreg;
-  };
-
-  if (nsteps > 0) {
-    load_step(0);
-    store_step(smem);
-  }
-  __syncthreads();
-
-  for (int st = 0; st < nsteps; ++st) {
-    const char* buf = smem + (st & 1) * BUF;
-    const char* sq = buf;
-    const char* sdo = buf + G::BYTES;
-    const float* slse = reinterpret_cast<const float*>(buf + 2 * G::BYTES);
-    const float* sdl = slse + BMQ;
-    int h_unused, qb0;
-    step_coords(st, h_unused, qb0);
-    const bool has_next = st + 1 < nsteps;
-    if (has_next) load_step(st + 1);
-
-    if (wave_live && !(CAUSAL && qb0 + BMQ - 1 < wk0)) {
-      f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f), d0 = (f32x16)(0.f), d1 = (f32x16)(0.f);
-      mfma_nat<T, D>(sq, l32, hh, kf, s0, s1);
-      mfma_nat<T, D>(sdo, l32, hh, vf, d0, d1);
-
-      // lane = key kkey; tile t register r = query qb0 + 32hh + 16t + r
-      const bool need_mask = !kvalid || (qb0 + BMQ > p.Sq) || (CAUSAL && qb0 < wk0 + 31);
-      f32x16 pp0, pp1;
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
-        const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const f32x4 lv = l4[r4], dl = d4[r4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * r4 + e;
-            const float sx = t ? s1[r] : s0[r];
-            const float dp = t ? d1[r] : d0[r];
-            float pv = __builtin_amdgcn_exp2f(fmaf(sx, p.scale_log2, -lv[e]));
-            if (need_mask) {
-              const int q = qb0 + 32 * hh + 16 * t + r;
-              const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
-              pv = ok ? pv : 0.f;
-            }
-            const float ds = pv * (dp - dl[e]);
-            if (t) { pp1[r] = pv; s1[r] = ds; } else { pp0[r] = pv; s0[r] = ds; }
-          }
-        }
-      }
-      Frag pfr[PF], dsf[PF];
-      pack_frags<T>(pp0, pp1, pfr);
-      pack_frags<T>(s0, s1, dsf);
-      mfma_trn<T, D>(sdo, lane, ta, pfr, dv);
-      mfma_trn<T, D>(sq, lane, ta, dsf, dk);
-    }
-    if (has_next) store_step(smem + ((st + 1) & 1) * BUF);
-    __syncthreads();
-  }
-
-  if (kkey < p.Sk) {
-    store_acc_row<T, D>(static_cast<T*>(p.dk) + (koff + kkey) * D, dk, p.sm_scale, hh);
-    store_acc_row<T, D>(static_cast<T*>(p.dv) + (koff + kkey) * D, dv, 1.f, hh);
-  }
-}
-
-template <typename T, int D>
-hipError_t delta_typed(const BwdParams& p, hipStream_t st) {
-  constexpr int LPR = D / (16 / (int)sizeof(T));
-  constexpr int RPB = 256 / LPR;
-  const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-  hipLaunchKernelGGL((pf_attn_bwd_delta_kernel<T, D>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256),
-                     0, st, p);
-  return hipGetLastError();
-}
-
-template <typename T, int D>
-hipError_t dq_typed(const BwdParams& p, bool causal, hipStream_t st) {
-  const int n_qblk = (p.Sq + 127) / 128;
-  const int n_work = p.B * p.Hq * n_qblk;
-  if (causal)
-    hipLaunchKernelGGL((pf_attn_bwd_dq_kernel<T, D, true>), dim3(n_work), dim3(256), 0, st, p, n_qblk, n_work);
-  else
-    hipLaunchKernelGGL((pf_attn_bwd_dq_kernel<T, D, false>), dim3(n_work), dim3(256), 0, st, p, n_qblk, n_work);
-  return hipGetLastError();
-}
-
-template <typename T, int D>
-hipError_t dkv_typed(const BwdParams& p, bool causal, hipStream_t st) {
-  const int n_kblk = (p.Sk + 127) / 128;
-  const int n_work = p.B * p.Hkv * n_kblk;
-  if (causal)
-    hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, true>), dim3(n_work), dim3(256), 0, st, p, n_kblk);
-  else
-    hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, false>), dim3(n_work), dim3(256), 0, st, p, n_kblk);
-  return hipGetLastError();
-}
-
-#define PF_DISPATCH(FN, ...)                                                   \
+#define PF_DISPATCH16(FN, ...)                                                 \
   do {                                                                         \
     if (head_dim == 128) {                                                     \
-      if (dtype == kF32) return FN<float, 128>(__VA_ARGS__);                   \
-      if (dtype == kBF16) return FN<bf16_t, 128>(__VA_ARGS__);                 \
-      if (dtype == kF16) return FN<f16_t, 128>(__VA_ARGS__);                   \
+      if (dtype == kBF16) return bwd::FN<bf16_t, 128>(__VA_ARGS__);            \
+      if (dtype == kF16) return bwd::FN<f16_t, 128>(__VA_ARGS__);              \
     } else if (head_dim == 64) {                                               \
-      if (dtype == kF32) return FN<float, 64>(__VA_ARGS__);                    \
-      if (dtype == kBF16) return FN<bf16_t, 64>(__VA_ARGS__);                  \
-      if (dtype == kF16) return FN<f16_t, 64>(__VA_ARGS__);                    \
+      if (dtype == kBF16) return bwd::FN<bf16_t, 64>(__VA_ARGS__);             \
+      if (dtype == kF16) return bwd::FN<f16_t, 64>(__VA_ARGS__);               \
     }                                                                          \
     return hipErrorInvalidValue;                                               \
   } while (0)
 
-}  // namespace
-
 hipError_t launch_attn_bwd_delta(const BwdParams& p, int dtype, int head_dim, hipStream_t stream) {
-  PF_DISPATCH(delta_typed, p, stream);
+  if (dtype == kF32) return launch_bwd_delta_f32(p, head_dim, stream);
+  PF_DISPATCH16(delta_typed, p, stream);
 }
 
 hipError_t launch_attn_bwd_dq(const BwdParams& p, int dtype, int head_dim, bool causal,
                               hipStream_t stream) {
-  PF_DISPATCH(dq_typed, p, causal, stream);
+  if (dtype == kF32) return launch_bwd_dq_f32(p, head_dim, causal, stream);
+  PF_DISPATCH16(dq_typed, p, causal, stream);
 }
 
 hipError_t launch_attn_bwd_dkv(const BwdParams& p, int dtype, int head_dim, bool causal,
                                hipStream_t stream) {
-  PF_DISPATCH(dkv_typed, p, causal, stream);
+  if (dtype == kF32) return launch_bwd_dkv_f32(p, head_dim, causal, stream);
+  return launch_bwd_dkv16(p, dtype, head_dim, causal, stream);
 }
 
 }  // namespace pf

@@ -188,16 +188,16 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
   const rsrc_t krs = make_rsrc(Kb, kv_bytes);
   const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
-  typename std::conditional<ROPE, RopeTileRegs<T, D>, TileRegs<T, D>>::type kreg;
-  TileRegs<T, D> vreg;
-  auto load_block = [&](int kv0) {
-    kreg.load(krs, kv0, tid);
-    vreg.load(vrs, kv0, tid);
+  // K and V go global -> LDS by DMA; with fused RoPE, K goes through registers
+  // to be rotated on the way.
+  RopeTileRegs<T, D> kreg;
+  auto load_block = [&](int kv0, char* sk, char* sv) {
+    if constexpr (ROPE) kreg.load(krs, kv0, tid);
+    else TileDma<T, D>::load(krs, kv0, sk, tid);
+    TileDma<T, D>::load(vrs, kv0, sv, tid);
   };
-  auto store_block = [&](int kv0, char* sk, char* sv) {
+  auto store_block = [&](int kv0, char* sk) {
     if constexpr (ROPE) kreg.store(sk, kv0, p.kv_len, p.k_cos, p.k_sin, tid);
-    else kreg.store(sk, tid);
-    vreg.store(sv, tid);
   };
 
   float m_run = kNegInf;  // running max, log2 domain (identical in both halves)
@@ -215,9 +215,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   vta.init(lane);
 
   if (nblk > 0) {
-    load_block(0);
-    store_block(0, smem, smem + G::BYTES);
+    load_block(0, smem, smem + G::BYTES);
+    store_block(0, smem);
   }
+  dma_wait();
   __syncthreads();
 
   for (int j = 0; j < nblk; ++j) {
@@ -225,7 +226,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     char* const sk = smem + (j & 1) * (2 * G::BYTES);
     char* const sv = sk + G::BYTES;
     const bool has_next = j + 1 < nblk;
-    if (has_next) load_block(kv0 + BN);
+    char* const nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
+    if (has_next) load_block(kv0 + BN, nk, nk + G::BYTES);
 
     const bool live = wq0 < p.Sq && !(CAUSAL && kv0 > wq_last);
     if (live) {
@@ -300,10 +302,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       mfma_trn<T, D>(sv, lane, vta, pfr, acc);
     }
 
-    if (has_next) {
-      char* const nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
-      store_block(kv0 + BN, nk, nk + G::BYTES);
-    }
+    if (has_next) store_block(kv0 + BN, nk);
+    dma_wait();
     __syncthreads();
   }
 

@@ -72,6 +72,32 @@ struct TileRegs {
   }
 };
 
+// Direct global -> LDS staging (buffer_load_dwordx4 ... lds): lane l of a
+// wave writes its 16 bytes at the instruction's LDS base (M0) + 16*l, so each
+// lane fetches the global chunk that belongs at its slot of the swizzled
+// tile. No registers hold the data and no LDS store instructions are issued;
+// the issuing wave must wait for vmcnt(0) (dma_wait) before the barrier that
+// publishes the tile.
+template <typename T, int D>
+struct TileDma {
+  using G = Tile<T, D>;
+  __device__ static inline void load(rsrc_t rs, int row0, char* tile, int tid) {
+    const int w = tid >> 6, l = tid & 63;
+#pragma unroll
+    for (int u = 0; u < G::PER_T; ++u) {
+      const int slot = 64 * (4 * u + w) + l;  // 16-byte slot within the tile
+      const int row = slot / G::CPR, phys = slot % G::CPR;
+      const int chunk = phys ^ tile_swz<G::CPR>(row);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(tile + 16 * 64 * (4 * u + w)), 16,
+          (uint32_t)((row0 + row) * D + chunk * G::EPC) * G::ES, 0, 0, 0);
+    }
+  }
+};
+
+// Wait for this wave's outstanding global loads (including LDS DMA).
+__device__ inline void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
+
 // Natural A operand: s0/s1 (32x32 tiles t = 0, 1) += tile rows x B fragments,
 // contracting over D (lane half hh owns columns [hh*D/2, (hh+1)*D/2)).
 template <typename T, int D>
@@ -93,6 +119,33 @@ __device__ inline void mfma_nat(const char* tile, int l32, int hh, const typenam
     for (int f = 0; f < FPC; ++f) {
       s0 = MF::run(chunk_frag<T>(a0, f), bf[c * FPC + f], s0);
       s1 = MF::run(chunk_frag<T>(a1, f), bf[c * FPC + f], s1);
+    }
+  }
+}
+
+// Natural A operands of two tiles at once, one 32-row half t each:
+// s += tile_a rows x bf_a and d += tile_b rows x bf_b (two independent MFMA
+// chains, interleaved).
+template <typename T, int D>
+__device__ inline void mfma_nat_pair(const char* tile_a, const typename Mfma32<T>::Frag* bf_a,
+                                     const char* tile_b, const typename Mfma32<T>::Frag* bf_b, int t,
+                                     int l32, int hh, f32x16& s, f32x16& d) {
+  using MF = Mfma32<T>;
+  using G = Tile<T, D>;
+  constexpr int FPC = frags_per_chunk<T>();
+  const int r = mfma_src_row(l32, t);
+  const int sw = tile_swz<G::CPR>(r);
+  const char* ba = tile_a + r * G::RB;
+  const char* bb = tile_b + r * G::RB;
+#pragma unroll
+  for (int c = 0; c < G::CPR / 2; ++c) {
+    const int off = 16 * ((hh * (G::CPR / 2) + c) ^ sw);
+    const u32x4 a = lds16(ba + off);
+    const u32x4 b = lds16(bb + off);
+#pragma unroll
+    for (int f = 0; f < FPC; ++f) {
+      s = MF::run(chunk_frag<T>(a, f), bf_a[c * FPC + f], s);
+      d = MF::run(chunk_frag<T>(b, f), bf_b[c * FPC + f], d);
     }
   }
 }
@@ -120,7 +173,9 @@ struct TrAddr {
 // Transposed A operand: acc[dt] += tile^T (rows = D columns of the tile,
 // reduction over the tile's 64 rows) x B fragments. Lane half hh's B slots
 // for step c are tile rows 32hh + 8c + [0, 8) (16-bit) or 32hh + s (f32).
-template <typename T, int D>
+// Steps [C0, C1) of 4 (16-bit: step c = tile rows 32hh + 8c + [0, 8); f32:
+// rows 32hh + 8c .. 32hh + 8c + 7 as 8 single-row steps); bf is indexed by step.
+template <typename T, int D, int C0 = 0, int C1 = 4>
 __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& ta,
                                 const typename Mfma32<T>::Frag* bf, f32x16* acc) {
   using MF = Mfma32<T>;
@@ -128,10 +183,12 @@ __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& 
   using Frag = typename MF::Frag;
   if constexpr (G::TR) {
     typedef short v4i16 __attribute__((ext_vector_type(4)));
+    // c outer, dt inner: consecutive MFMAs feed independent accumulators, so
+    // none waits on the previous one's result.
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+    for (int c = C0; c < C1; ++c)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int dt = 0; dt < D / 32; ++dt) {
         v4i16 part[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r)
@@ -143,11 +200,11 @@ __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& 
   } else {
     const int l32 = lane & 31, hh = lane >> 5;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-      const int d = 32 * dt + l32;
+    for (int s = 8 * C0; s < 8 * C1; ++s) {
+      const int row = 32 * hh + s;
 #pragma unroll
-      for (int s = 0; s < 32; ++s) {
-        const int row = 32 * hh + s;
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const int d = 32 * dt + l32;
         const float a = *reinterpret_cast<const float*>(
             tile + row * G::RB + 16 * ((d >> 2) ^ tile_swz<G::CPR>(row)) + 4 * (d & 3));
         acc[dt] = MF::run(a, bf[s], acc[dt]);
