@@ -132,7 +132,9 @@ def bench_rope(L, _lib, torch, iters):
     o = torch.empty_like(q)
     base = _lib.FwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None,
                         B, Hq, Hkv, S, S, D, S, 1, 1.0 / D ** 0.5, 1)
-    ra = _lib.FwdRopeArgs(base, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(), sin.data_ptr())
+    ra = _lib.FwdRopeArgs(base, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(), sin.data_ptr(), None, 0)
+    ws = torch.empty(L.pf_attn_fwd_rope_workspace_size(ra), dtype=torch.uint8, device="cuda")
+    ra.workspace, ra.workspace_bytes = ws.data_ptr(), ws.numel()
     st = torch.cuda.current_stream().cuda_stream
     for _ in range(3):
         ok(L.pf_attn_fwd_rope(ra, st), "pf_attn_fwd_rope")

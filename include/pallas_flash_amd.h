@@ -73,10 +73,15 @@ int pf_attn_fwd(const pf_attn_fwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Fused-RoPE forward (no LSE). Replaces the `flash_attention_rope_fwd`
- * pallas_call (fused_rope.py:183-213, kernel :53-113). Q and K are rotated in
- * float32 (x*cos + rotate_half(x)*sin) while their tiles are staged.
+ * pallas_call (fused_rope.py:183-213, kernel :53-113). Rotation is
+ * x*cos + rotate_half(x)*sin in float32. Q is rotated in registers inside the
+ * attention kernel; K rows [0, kv_len) are rotated exactly once by a prologue
+ * kernel into `workspace`, which the attention kernel then streams (the
+ * reference re-rotates every K tile for every query head and query block).
  *   q_cos, q_sin [seq_len_q, head_dim] float32
  *   k_cos, k_sin [seq_len_k, head_dim] float32
+ *   workspace: at least pf_attn_fwd_rope_workspace_size(args) bytes,
+ *              256-byte aligned device memory (contents on entry do not matter)
  * Other fields as pf_attn_fwd_args (lse is ignored and may be NULL).
  * ------------------------------------------------------------------------- */
 typedef struct {
@@ -85,8 +90,11 @@ typedef struct {
   const float* q_sin;
   const float* k_cos;
   const float* k_sin;
+  void* workspace;
+  size_t workspace_bytes;
 } pf_attn_fwd_rope_args;
 
+size_t pf_attn_fwd_rope_workspace_size(const pf_attn_fwd_rope_args* args);
 int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------

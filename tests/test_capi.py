@@ -31,7 +31,8 @@ def L():
 
 def test_header_declares_expected_entry_points():
     names = _declared_functions()
-    for want in ("pf_attn_fwd", "pf_attn_fwd_rope", "pf_attn_bwd", "pf_attn_bwd_delta",
+    for want in ("pf_attn_fwd", "pf_attn_fwd_rope", "pf_attn_fwd_rope_workspace_size",
+                 "pf_attn_bwd", "pf_attn_bwd_delta",
                  "pf_attn_bwd_dq", "pf_attn_bwd_dkv", "pf_attn_decode",
                  "pf_attn_decode_workspace_size", "pf_paged_attn", "pf_paged_attn_workspace_size",
                  "pf_version"):
@@ -51,7 +52,7 @@ def test_version(L):
 def test_struct_sizes_match_c_layout():
     # pointers 8 bytes; int32/float 4; size_t 8 (x86-64 SysV)
     assert ctypes.sizeof(_lib.FwdArgs) == 5 * 8 + 10 * 4
-    assert ctypes.sizeof(_lib.FwdRopeArgs) == ctypes.sizeof(_lib.FwdArgs) + 4 * 8
+    assert ctypes.sizeof(_lib.FwdRopeArgs) == ctypes.sizeof(_lib.FwdArgs) + 4 * 8 + 8 + 8
     assert ctypes.sizeof(_lib.BwdArgs) == 10 * 8 + 10 * 4
     assert ctypes.sizeof(_lib.DecodeArgs) == 4 * 8 + 8 * 4 + 8 + 8
     assert ctypes.sizeof(_lib.PagedArgs) == 6 * 8 + 9 * 4 + 4 + 8 + 8
@@ -83,8 +84,21 @@ def test_fwd_null_args(L):
 
 
 def test_rope_requires_tables(L):
-    args = _lib.FwdRopeArgs(_fwd(), None, None, None, None)
+    args = _lib.FwdRopeArgs(_fwd(), None, None, None, None, 256, 1 << 20)
     assert L.pf_attn_fwd_rope(args, None) == _lib.PF_ERR_INVALID
+
+
+def test_rope_workspace_size_and_rejection(L):
+    # rotated-K workspace = K's bytes (bf16 [1, 2, 16, 128]), rounded up to 256
+    args = _lib.FwdRopeArgs(_fwd(), 8, 8, 8, 8, None, 0)
+    assert L.pf_attn_fwd_rope_workspace_size(args) == 2 * 16 * 128 * 2
+    assert L.pf_attn_fwd_rope(args, None) == _lib.PF_ERR_WORKSPACE
+    args.workspace, args.workspace_bytes = 256, 2 * 16 * 128 * 2 - 1
+    assert L.pf_attn_fwd_rope(args, None) == _lib.PF_ERR_WORKSPACE
+    args.workspace, args.workspace_bytes = 264, 1 << 20  # not 256-byte aligned
+    assert L.pf_attn_fwd_rope(args, None) == _lib.PF_ERR_WORKSPACE
+    args.base.head_dim = 96
+    assert L.pf_attn_fwd_rope_workspace_size(args) == 0
 
 
 def test_bwd_requires_buffers(L):

@@ -1,13 +1,16 @@
-// Forward prefill attention for gfx950 (CDNA4), with optional fused RoPE.
+// Forward prefill attention for gfx950 (CDNA4), with optional fused RoPE
+// (Q rotated in registers here; K rotated once by pf_rope_rotate_k_kernel).
 //
 // Replaces the reference's `flash_attention_fwd` pallas_call
 // (flash_attention.py:162-227, kernel :61-159) and `flash_attention_rope_fwd`
 // (fused_rope.py:183-213, kernel :53-113).
 //
-// Work decomposition: one workgroup of 4 waves per (batch, query head, 128-row
-// query block); each wave owns 32 query rows. The grid is 1-D: heavy (late)
-// query blocks first for causal load balance, and the query heads of one GQA
-// group on one XCD so they share K/V in that XCD's L2 (see xcd_remap).
+// Work decomposition: one workgroup of 4 waves per (batch, GQA head group,
+// query block); each wave owns 32 query rows of one head. A workgroup packs
+// hpw query heads of one GQA group (4 when the group size allows) x 128/hpw
+// rows, so the K/V tiles it stages serve all those heads. The grid is 1-D: heavy (late) query
+// blocks first for causal load balance, and the head groups sharing a KV
+// head on one XCD so they share K/V in that XCD's L2 (see xcd_remap).
 //
 // Per 64-key block the workgroup stages K and V in LDS, double-buffered: the
 // global loads for block j+1 are in flight while block j is computed, and one
@@ -43,68 +46,14 @@ namespace pf {
 
 namespace {
 
-constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdBN = 64;   // keys per block
-
-// Fused-RoPE K staging: each item is a (row, chunk) pair of the first half of
-// the row together with its partner chunk D/2 further, rotated in float32
-// (x*cos + rotate_half(x)*sin, fused_rope.py:43-50, :75-78) before the store.
-template <typename T, int D>
-struct RopeTileRegs {
-  using G = Tile<T, D>;
-  static constexpr int ITEMS = 64 * G::CPR / 2;
-  static constexpr int PER_T = (ITEMS + 255) / 256;
-  u32x4 lo[PER_T], hi[PER_T];
-
-  __device__ inline void load(rsrc_t rs, int row0, int tid) {
-#pragma unroll
-    for (int u = 0; u < PER_T; ++u) {
-      const int c = tid + 256 * u;
-      if (ITEMS % 256 == 0 || c < ITEMS) {
-        const int row = c / (G::CPR / 2), pc = c % (G::CPR / 2);
-        const uint32_t off = (uint32_t)((row0 + row) * D + pc * G::EPC) * G::ES;
-        lo[u] = bufld16(rs, off);
-        hi[u] = bufld16(rs, off + (D / 2) * G::ES);
-      }
-    }
-  }
-  __device__ inline void store(char* tile, int row0, int valid_rows, const float* cosb, const float* sinb,
-                               int tid) const {
-#pragma unroll
-    for (int u = 0; u < PER_T; ++u) {
-      const int c = tid + 256 * u;
-      if (ITEMS % 256 == 0 || c < ITEMS) {
-        const int row = c / (G::CPR / 2), pc = c % (G::CPR / 2);
-        u32x4 lo_out = {0u, 0u, 0u, 0u}, hi_out = {0u, 0u, 0u, 0u};
-        if (row0 + row < valid_rows) {  // tables are [Sk, D]: read only for valid keys
-          float a[G::EPC], b[G::EPC], ra[G::EPC], rb[G::EPC];
-          chunk_to_f32<T>(lo[u], a);
-          chunk_to_f32<T>(hi[u], b);
-          const float* cs = cosb + (int64_t)(row0 + row) * D + pc * G::EPC;
-          const float* sn = sinb + (int64_t)(row0 + row) * D + pc * G::EPC;
-#pragma unroll
-          for (int e = 0; e < G::EPC; ++e) {
-            ra[e] = a[e] * cs[e] - b[e] * sn[e];
-            rb[e] = b[e] * cs[D / 2 + e] + a[e] * sn[D / 2 + e];
-          }
-          lo_out = f32_to_chunk<T>(ra);
-          hi_out = f32_to_chunk<T>(rb);
-        }
-        char* dst = tile + row * G::RB;
-        const int sw = tile_swz<G::CPR>(row);
-        sts16(dst + 16 * (pc ^ sw), lo_out);
-        sts16(dst + 16 * ((pc + G::CPR / 2) ^ sw), hi_out);
-      }
-    }
-  }
-};
 
 template <typename T, int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_attn_fwd_kernel(FwdParams p) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
   using G = Tile<T, D>;
-  constexpr int BM = kFwdBM, BN = kFwdBN;
+  constexpr int BN = kFwdBN;
   constexpr int HALF = D / 2;
   constexpr int ES = G::ES, EPC = G::EPC;
   constexpr int FPC = frags_per_chunk<T>();
@@ -122,17 +71,21 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const int hh = lane >> 5;
   const int l32 = lane & 31;
 
-  const int w = xcd_remap(blockIdx.x, p.n_work, p.g);
-  const int member = w % p.g;
-  int rest = w / p.g;
+  // work item = (query block, batch, kv head, head group); the workgroup's
+  // waves split into hpw heads x (4 / hpw) 32-row slices.
+  const int n_hg = p.g / p.hpw;
+  const int w = xcd_remap(blockIdx.x, p.n_work, n_hg);
+  const int hg = w % n_hg;
+  int rest = w / n_hg;
   const int kvh = rest % p.Hkv;
   rest /= p.Hkv;
   const int b = rest % p.B;
   const int qblk = p.n_qblk - 1 - rest / p.B;
-  const int h = kvh * p.g + member;
+  const int wph = 4 / p.hpw;  // waves per head
+  const int h = kvh * p.g + hg * p.hpw + wv / wph;
 
-  const int q0 = qblk * BM;
-  const int wq0 = q0 + 32 * wv;
+  const int q0 = qblk * p.rpw;
+  const int wq0 = q0 + 32 * (wv % wph);
   const int qrow = wq0 + l32;
   const int wq_last = min(wq0 + 31, p.Sq - 1);
 
@@ -188,16 +141,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
   const rsrc_t krs = make_rsrc(Kb, kv_bytes);
   const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
-  // K and V go global -> LDS by DMA; with fused RoPE, K goes through registers
-  // to be rotated on the way.
-  RopeTileRegs<T, D> kreg;
+  // K and V go global -> LDS by DMA (with fused RoPE, p.k is the K rotated
+  // once by pf_rope_rotate_k_kernel).
   auto load_block = [&](int kv0, char* sk, char* sv) {
-    if constexpr (ROPE) kreg.load(krs, kv0, tid);
-    else TileDma<T, D>::load(krs, kv0, sk, tid);
+    TileDma<T, D>::load(krs, kv0, sk, tid);
     TileDma<T, D>::load(vrs, kv0, sv, tid);
-  };
-  auto store_block = [&](int kv0, char* sk) {
-    if constexpr (ROPE) kreg.store(sk, kv0, p.kv_len, p.k_cos, p.k_sin, tid);
   };
 
   float m_run = kNegInf;  // running max, log2 domain (identical in both halves)
@@ -207,7 +155,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   for (int i = 0; i < NDT; ++i) acc[i] = (f32x16)(0.f);
 
   int kv_end = p.kv_len;
-  if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + BM, p.Sq));
+  if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + p.rpw, p.Sq));
   const int nblk = (kv_end + BN - 1) / BN;
   const float c2 = fabsf(p.scale_log2);
 
@@ -216,7 +164,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 
   if (nblk > 0) {
     load_block(0, smem, smem + G::BYTES);
-    store_block(0, smem);
   }
   dma_wait();
   __syncthreads();
@@ -302,7 +249,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       mfma_trn<T, D>(sv, lane, vta, pfr, acc);
     }
 
-    if (has_next) store_block(kv0 + BN, nk);
     dma_wait();
     __syncthreads();
   }
@@ -337,6 +283,41 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   }
 }
 
+// K rotation prologue of the fused-RoPE forward: each thread rotates one
+// 16-byte chunk of the first half of a row together with its partner chunk
+// D/2 further (x*cos + rotate_half(x)*sin in float32, fused_rope.py:43-50,
+// :75-78), then rounds once to T. Rows at or past kv_len are not touched (the
+// attention kernel never reads them).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void pf_rope_rotate_k_kernel(const T* __restrict__ k, T* __restrict__ out,
+                                                               const float* __restrict__ cosb,
+                                                               const float* __restrict__ sinb, int Sk,
+                                                               int kv_len, int64_t n_items) {
+  constexpr int EPC = 16 / (int)sizeof(T);
+  constexpr int HC = D / 2 / EPC;  // chunks per half row
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (item >= n_items) return;
+  const int pc = (int)(item % HC);
+  const int64_t rr = item / HC;           // row over (batch, kv head, position < kv_len)
+  const int pos = (int)(rr % kv_len);
+  const int64_t bh = rr / kv_len;
+  const int64_t row = bh * Sk + pos;
+  const T* src = k + row * D + pc * EPC;
+  float a[EPC], bb[EPC], ra[EPC], rb[EPC];
+  chunk_to_f32<T>(ldg16(src), a);
+  chunk_to_f32<T>(ldg16(src + D / 2), bb);
+  const float* cs = cosb + (int64_t)pos * D + pc * EPC;
+  const float* sn = sinb + (int64_t)pos * D + pc * EPC;
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) {
+    ra[e] = a[e] * cs[e] - bb[e] * sn[e];
+    rb[e] = bb[e] * cs[D / 2 + e] + a[e] * sn[D / 2 + e];
+  }
+  T* dst = out + row * D + pc * EPC;
+  stg16(dst, f32_to_chunk<T>(ra));
+  stg16(dst + D / 2, f32_to_chunk<T>(rb));
+}
+
 template <typename T, int D>
 hipError_t launch_typed(const FwdParams& p, bool causal, bool rope, hipStream_t st) {
   const dim3 grid(p.n_work), block(256);
@@ -357,7 +338,32 @@ hipError_t launch_dim(const FwdParams& p, int head_dim, bool causal, bool rope, 
   return hipErrorInvalidValue;
 }
 
+template <typename T, int D>
+hipError_t rotate_typed(const void* k, void* out, const float* cs, const float* sn, int B, int Hkv, int Sk,
+                        int kv_len, hipStream_t st) {
+  constexpr int HC = D / 2 / (16 / (int)sizeof(T));
+  const int64_t n_items = (int64_t)B * Hkv * kv_len * HC;
+  if (n_items == 0) return hipSuccess;
+  hipLaunchKernelGGL((pf_rope_rotate_k_kernel<T, D>), dim3((unsigned)((n_items + 255) / 256)), dim3(256), 0,
+                     st, static_cast<const T*>(k), static_cast<T*>(out), cs, sn, Sk, kv_len, n_items);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_rope_rotate_k(const void* k, void* k_out, const float* cos, const float* sin, int B,
+                                int Hkv, int Sk, int kv_len, int dtype, int head_dim, hipStream_t stream) {
+  if (head_dim == 128) {
+    if (dtype == kF32) return rotate_typed<float, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, stream);
+    if (dtype == kBF16) return rotate_typed<bf16_t, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, stream);
+    if (dtype == kF16) return rotate_typed<f16_t, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, stream);
+  } else if (head_dim == 64) {
+    if (dtype == kF32) return rotate_typed<float, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, stream);
+    if (dtype == kBF16) return rotate_typed<bf16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, stream);
+    if (dtype == kF16) return rotate_typed<f16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, stream);
+  }
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream) {

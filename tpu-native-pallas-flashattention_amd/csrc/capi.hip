@@ -38,7 +38,7 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   p->v = a->v;
   p->o = a->o;
   p->lse = a->lse;
-  p->q_cos = p->q_sin = p->k_cos = p->k_sin = nullptr;
+  p->q_cos = p->q_sin = nullptr;
   p->B = a->batch;
   p->Hq = a->num_heads;
   p->Hkv = a->num_kv_heads;
@@ -47,8 +47,12 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   p->kv_len = a->kv_len;
   p->g = a->num_heads / a->num_kv_heads;
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
-  p->n_qblk = (a->seq_len_q + 127) / 128;
-  const int64_t n_work = (int64_t)a->batch * a->num_heads * p->n_qblk;
+  // A workgroup's 4 waves cover hpw query heads of one GQA group x rpw rows:
+  // the K/V tiles it stages serve all of them.
+  p->hpw = (p->g % 4 == 0) ? 4 : (p->g % 2 == 0) ? 2 : 1;
+  p->rpw = 128 / p->hpw;
+  p->n_qblk = (a->seq_len_q + p->rpw - 1) / p->rpw;
+  const int64_t n_work = (int64_t)a->batch * (a->num_heads / p->hpw) * p->n_qblk;
   if (n_work > kMaxGrid) return PF_ERR_UNSUPPORTED;
   // per-(batch, kv head) byte offsets are 32-bit inside the kernels
   if ((int64_t)(a->seq_len_k + 256) * a->head_dim * 4 > 0x7fffffff) return PF_ERR_UNSUPPORTED;
@@ -72,6 +76,18 @@ int pf_attn_fwd(const pf_attn_fwd_args* a, void* stream) {
                                     (hipStream_t)stream));
 }
 
+static size_t rope_ws_bytes(const pf_attn_fwd_args& b) {
+  const size_t es = b.dtype == PF_DTYPE_F32 ? 4 : 2;
+  return (((size_t)b.batch * b.num_kv_heads * b.seq_len_k * b.head_dim * es) + 255) & ~(size_t)255;
+}
+
+size_t pf_attn_fwd_rope_workspace_size(const pf_attn_fwd_rope_args* a) {
+  if (!a) return 0;
+  pf::FwdParams p;
+  if (fill_fwd(&a->base, &p) != PF_OK) return 0;
+  return rope_ws_bytes(a->base);
+}
+
 int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* a, void* stream) {
   if (!a) return PF_ERR_INVALID;
   pf::FwdParams p;
@@ -79,14 +95,20 @@ int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* a, void* stream) {
   if (st != PF_OK) return st;
   if (!a->q_cos || !a->q_sin || !a->k_cos || !a->k_sin) return PF_ERR_INVALID;
   if (a->base.head_dim % 2 != 0) return PF_ERR_INVALID;  // fused_rope.py:168-169
+  if (p.n_work == 0) return PF_OK;
+  const size_t need = rope_ws_bytes(a->base);
+  if (!a->workspace || a->workspace_bytes < need || ((uintptr_t)a->workspace & 255) != 0)
+    return PF_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  st = finish(pf::launch_rope_rotate_k(a->base.k, a->workspace, a->k_cos, a->k_sin, a->base.batch,
+                                       a->base.num_kv_heads, a->base.seq_len_k, a->base.kv_len,
+                                       a->base.dtype, a->base.head_dim, s));
+  if (st != PF_OK) return st;
+  p.k = a->workspace;  // rotated K
   p.q_cos = a->q_cos;
   p.q_sin = a->q_sin;
-  p.k_cos = a->k_cos;
-  p.k_sin = a->k_sin;
   p.lse = nullptr;  // the reference's fused kernel has no LSE output
-  if (p.n_work == 0) return PF_OK;
-  return finish(pf::launch_attn_fwd(p, a->base.dtype, a->base.head_dim, a->base.causal != 0, true,
-                                    (hipStream_t)stream));
+  return finish(pf::launch_attn_fwd(p, a->base.dtype, a->base.head_dim, a->base.causal != 0, true, s));
 }
 
 // ---------------------------------------------------------------------------

@@ -15,18 +15,23 @@ struct FwdParams {
   const void* v;
   void* o;
   float* lse;  // may be null
-  const float* q_cos;
+  const float* q_cos;  // fused RoPE: [Sq, D] tables for Q (K arrives rotated)
   const float* q_sin;
-  const float* k_cos;
-  const float* k_sin;
   int B, Hq, Hkv, Sq, Sk, kv_len, g;
   float scale_log2;  // sm_scale * log2(e)
-  int n_qblk;        // ceil(Sq / 128)
-  int n_work;        // B * Hq * n_qblk
+  int hpw;           // query heads per workgroup (1, 2 or 4; divides g)
+  int rpw;           // query rows per head per workgroup (128 / hpw)
+  int n_qblk;        // ceil(Sq / rpw)
+  int n_work;        // B * Hq / hpw * n_qblk
 };
 
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream);
+
+// Rotate K rows [0, kv_len) of every (batch, kv head) into k_out (same layout
+// as k): x*cos + rotate_half(x)*sin with the [Sk, D] float32 tables.
+hipError_t launch_rope_rotate_k(const void* k, void* k_out, const float* cos, const float* sin, int B,
+                                int Hkv, int Sk, int kv_len, int dtype, int head_dim, hipStream_t stream);
 
 // Backward.
 struct BwdParams {

@@ -41,6 +41,7 @@ class FwdRopeArgs(ctypes.Structure):
     _fields_ = [
         ("base", FwdArgs),
         ("q_cos", c_ptr), ("q_sin", c_ptr), ("k_cos", c_ptr), ("k_sin", c_ptr),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -78,6 +79,7 @@ class PagedArgs(ctypes.Structure):
 # (symbol, argtypes, restype) for every entry point the header declares.
 SIGNATURES = {
     "pf_attn_fwd": ([ctypes.POINTER(FwdArgs), c_ptr], ctypes.c_int),
+    "pf_attn_fwd_rope_workspace_size": ([ctypes.POINTER(FwdRopeArgs)], ctypes.c_size_t),
     "pf_attn_fwd_rope": ([ctypes.POINTER(FwdRopeArgs), c_ptr], ctypes.c_int),
     "pf_attn_bwd_delta": ([ctypes.POINTER(BwdArgs), c_ptr], ctypes.c_int),
     "pf_attn_bwd_dq": ([ctypes.POINTER(BwdArgs), c_ptr], ctypes.c_int),

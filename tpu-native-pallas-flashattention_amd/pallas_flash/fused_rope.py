@@ -1,9 +1,11 @@
 """FlashAttention with rotary position embeddings fused into the kernel.
 
 Drop-in for the reference's ``pallas_flash.fused_rope.flash_attention_rope``
-(src/pallas_flash/fused_rope.py:116-213). Q and K are rotated in float32
-(``x * cos + rotate_half(x) * sin``) while their tiles are staged by the HIP
-kernel, so the rotated copies never touch HBM. Forward only, like the
+(src/pallas_flash/fused_rope.py:116-213). Rotation is float32
+``x * cos + rotate_half(x) * sin``. Q is rotated in registers inside the HIP
+attention kernel; K is rotated exactly once per position by a prologue kernel
+into a workspace the attention kernel streams (the reference re-rotates every
+K tile for every query head and query block). Forward only, like the
 reference (its docstring: "for training use the differentiable
 flash_attention with RoPE applied outside").
 """
@@ -34,9 +36,14 @@ class _RopeFn(torch.autograd.Function):
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), None,
             B, Hq, Hkv, Sq, Sk, D, kv_len, int(bool(causal)), float(sm_scale), _lib.dtype_tag(q))
         args = _lib.FwdRopeArgs(base, _lib.ptr(q_cos), _lib.ptr(q_sin), _lib.ptr(k_cos),
-                                _lib.ptr(k_sin))
+                                _lib.ptr(k_sin), None, 0)
+        L = _lib.lib()
+        nbytes = L.pf_attn_fwd_rope_workspace_size(args)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        args.workspace = _lib.ptr(ws)
+        args.workspace_bytes = nbytes
         with torch.cuda.device(q.device):
-            _lib.check(_lib.lib().pf_attn_fwd_rope(args, _lib.stream_of(q)), "flash_attention_rope")
+            _lib.check(L.pf_attn_fwd_rope(args, _lib.stream_of(q)), "flash_attention_rope")
         return o
 
     @staticmethod
@@ -65,7 +72,8 @@ def flash_attention_rope(
     """Attention with RoPE applied to Q and K inside the kernel.
 
     Equivalent to ``flash_attention(apply_rope(q), apply_rope(k), v)`` without
-    materialising the rotated Q and K.
+    materialising the rotated Q; the rotated K lives in a transient workspace
+    of K's size.
 
     Args:
         q: ``[batch, num_heads, seq_len_q, head_dim]``.
