@@ -231,6 +231,22 @@ def bench_paged(L, _lib, torch, iters):
     return ev.mean_ms(0, 1), nbytes
 
 
+def bench_copy(torch, iters):
+    """A plain device-to-device copy of 1 GiB (torch's copy kernel): the
+    calibration workload for the HBM byte counters (its FETCH_SIZE and
+    WRITE_SIZE per dispatch are each 1 GiB of algorithmic traffic)."""
+    nbytes = 1 << 30
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    ev = Events(2, iters)
+    for i in range(iters):
+        ev.mark(i, 0)
+        dst.copy_(src)
+        ev.mark(i, 1)
+    torch.cuda.synchronize()
+    return ev.mean_ms(0, 1), nbytes
+
+
 def cpu_baseline(c3):
     """The float32 numpy restatement of the reference algorithm (oracle/),
     forward + backward on a bounded sample of config 3: batch 0 (16 query
@@ -276,7 +292,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged"], default="all")
+    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "copy"], default="all")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -312,6 +328,12 @@ def main():
         ms, nb = bench_paged(L, _lib, torch, iters)
         sec["paged_gbs"] = nb / (ms * 1e-3) / 1e9
         sec["paged_ms"] = ms
+
+    if args.only == "copy":
+        log("copy calibration ...")
+        ms, nb = bench_copy(torch, iters)
+        sec["copy_gbs"] = 2 * nb / (ms * 1e-3) / 1e9
+        sec["copy_ms"] = ms
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",

@@ -3,6 +3,7 @@
 // (no HIP call before validation passes), fills a kernel parameter block and
 // enqueues on the caller's stream. Nothing here allocates or synchronises.
 #include <math.h>
+#include <stdlib.h>
 
 #include "../../include/pallas_flash_amd.h"
 #include "pf_kernels.hpp"
@@ -204,6 +205,24 @@ static int decode_chunk(int64_t units, int max_len) {
   return (int)chunk;
 }
 
+// Streaming kernel (decode_stream.hip): a persistent grid of one-wave
+// workgroups, as many as are resident at once, with an LDS ring of 2 stages
+// (measured on MI355X: 2 stages x 4 waves per CU beat 3 x 3 and 4 x 2).
+// Tuning and test overrides: PF_DECODE_STAGES (2..4) and PF_DECODE_WAVES
+// (grid size; any value >= 1 is correct, only the resident count is fast).
+static int stream_setup(pf::DecodeParams* p, int group) {
+  const char* env = getenv("PF_DECODE_STAGES");
+  int ns = env ? atoi(env) : 2;
+  if (ns < 2 || ns > 4) ns = 2;
+  p->stages = ns;
+  const char* wenv = getenv("PF_DECODE_WAVES");
+  const int wv = wenv ? atoi(wenv) : 0;
+  p->n_waves = wv > 0 ? wv : pf::decode_stream_waves(ns, group);
+  p->n_split = 0;
+  p->chunk = 0;
+  return p->n_waves;
+}
+
 static int fill_decode(const pf_attn_decode_args* a, pf::DecodeParams* p) {
   if (!a) return PF_ERR_INVALID;
   if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->cache_size < 1)
@@ -226,15 +245,28 @@ static int fill_decode(const pf_attn_decode_args* a, pf::DecodeParams* p) {
   p->D = a->head_dim;
   p->cache_size = a->cache_size;
   p->cache_len = a->cache_len;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  if (pf::decode_stream_supported(a->dtype, a->head_dim, false, 0)) {
+    // buffer offsets within one (b, kv head) run are 32-bit
+    if ((int64_t)a->cache_size * a->head_dim * 2 >= ((int64_t)1 << 31)) return PF_ERR_UNSUPPORTED;
+    if (stream_setup(p, g) <= 0) return PF_ERR_LAUNCH;
+    return PF_OK;
+  }
   p->chunk = decode_chunk(units, a->cache_len);
   p->n_split = (a->cache_len + p->chunk - 1) / p->chunk;
-  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
   if (units * p->n_split > kMaxGrid) return PF_ERR_UNSUPPORTED;
   return PF_OK;
 }
 
+// Partial slots: streaming kernel 2 per wave x query rows; generic kernel
+// one per (b, query head, chunk).
+static size_t decode_slots(const pf::DecodeParams& p) {
+  if (p.n_waves > 0) return (size_t)2 * p.n_waves * pf::decode_stream_qrows(p.Hq / p.Hkv);
+  return (size_t)p.B * p.Hq * p.n_split;
+}
+
 static size_t decode_ws_bytes(const pf::DecodeParams& p) {
-  const size_t slots = (size_t)p.B * p.Hq * p.n_split;
+  const size_t slots = decode_slots(p);
   return align256(slots * p.D * sizeof(float)) + align256(slots * 2 * sizeof(float));
 }
 
@@ -242,7 +274,7 @@ static int bind_workspace(pf::DecodeParams* p, void* ws, size_t bytes) {
   const size_t need = decode_ws_bytes(*p);
   if (need == 0) return PF_OK;
   if (!ws || bytes < need || ((uintptr_t)ws & 255) != 0) return PF_ERR_WORKSPACE;
-  const size_t slots = (size_t)p->B * p->Hq * p->n_split;
+  const size_t slots = decode_slots(*p);
   p->part_o = static_cast<float*>(ws);
   p->part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256(slots * p->D * sizeof(float)));
   return PF_OK;
@@ -293,9 +325,14 @@ static int fill_paged(const pf_paged_attn_args* a, pf::DecodeParams* p) {
   p->num_pages = a->num_pages;
   p->page_size = a->page_size;
   p->pages_per_seq = a->pages_per_seq;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  if (pf::decode_stream_supported(a->dtype, a->head_dim, true, a->page_size)) {
+    if ((int64_t)a->page_size * a->head_dim * 2 >= ((int64_t)1 << 31)) return PF_ERR_UNSUPPORTED;
+    if (stream_setup(p, g) <= 0) return PF_ERR_LAUNCH;
+    return PF_OK;
+  }
   p->chunk = decode_chunk(units, (int)(max_len > 0 ? max_len : 1));
   p->n_split = max_len > 0 ? (int)((max_len + p->chunk - 1) / p->chunk) : 1;
-  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
   if (units * p->n_split > kMaxGrid) return PF_ERR_UNSUPPORTED;
   return PF_OK;
 }

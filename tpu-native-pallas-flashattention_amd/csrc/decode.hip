@@ -314,8 +314,11 @@ hipError_t launch_typed(const DecodeParams& p, hipStream_t st) {
   const int64_t n_tasks = (int64_t)p.B * p.Hkv * n_hc * p.n_split;
   hipLaunchKernelGGL((pf_decode_kernel<T, D, PAGED>), dim3((unsigned)((n_tasks + 3) / 4)), dim3(256),
                      0, st, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+template <typename T, int D, bool PAGED>
+hipError_t launch_combine_typed(const DecodeParams& p, hipStream_t st) {
   const int64_t n_bh = (int64_t)p.B * p.Hq;
   hipLaunchKernelGGL((pf_decode_combine_kernel<T, D, PAGED>), dim3((unsigned)((n_bh + 3) / 4)),
                      dim3(256), 0, st, p);
@@ -323,26 +326,34 @@ hipError_t launch_typed(const DecodeParams& p, hipStream_t st) {
 }
 
 template <typename T, bool PAGED>
-hipError_t launch_dim(const DecodeParams& p, hipStream_t st) {
-  if (p.D == 128) return launch_typed<T, 128, PAGED>(p, st);
-  if (p.D == 64) return launch_typed<T, 64, PAGED>(p, st);
+hipError_t launch_dim(const DecodeParams& p, bool combine, hipStream_t st) {
+  if (p.D == 128) return combine ? launch_combine_typed<T, 128, PAGED>(p, st) : launch_typed<T, 128, PAGED>(p, st);
+  if (p.D == 64) return combine ? launch_combine_typed<T, 64, PAGED>(p, st) : launch_typed<T, 64, PAGED>(p, st);
   return hipErrorInvalidValue;
 }
 
 template <bool PAGED>
-hipError_t launch_dtype(const DecodeParams& p, int dtype, hipStream_t st) {
+hipError_t launch_dtype(const DecodeParams& p, int dtype, bool combine, hipStream_t st) {
   switch (dtype) {
-    case kF32: return launch_dim<float, PAGED>(p, st);
-    case kBF16: return launch_dim<bf16_t, PAGED>(p, st);
-    case kF16: return launch_dim<f16_t, PAGED>(p, st);
+    case kF32: return launch_dim<float, PAGED>(p, combine, st);
+    case kBF16: return launch_dim<bf16_t, PAGED>(p, combine, st);
+    case kF16: return launch_dim<f16_t, PAGED>(p, combine, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 }  // namespace
 
+hipError_t launch_decode_combine(const DecodeParams& p, int dtype, bool paged, hipStream_t stream) {
+  return paged ? launch_dtype<true>(p, dtype, true, stream) : launch_dtype<false>(p, dtype, true, stream);
+}
+
 hipError_t launch_decode(const DecodeParams& p, int dtype, bool paged, hipStream_t stream) {
-  return paged ? launch_dtype<true>(p, dtype, stream) : launch_dtype<false>(p, dtype, stream);
+  if (decode_stream_supported(dtype, p.D, paged, p.page_size))
+    return launch_decode_stream(p, dtype, paged, stream);
+  hipError_t e = paged ? launch_dtype<true>(p, dtype, false, stream) : launch_dtype<false>(p, dtype, false, stream);
+  if (e != hipSuccess) return e;
+  return launch_decode_combine(p, dtype, paged, stream);
 }
 
 }  // namespace pf

@@ -71,10 +71,19 @@ struct DecodeParams {
   int cache_len;      // contiguous: valid slots
   int num_pages, page_size, pages_per_seq;  // paged only
   int n_split;        // KV chunks per (b, kvh)
-  int chunk;          // keys per chunk (multiple of the page size when paged)
+  int chunk;          // keys per chunk (multiple of 32)
   float scale_log2;
+  int stages;         // streaming kernel: LDS ring depth (2..4)
+  int n_waves;        // streaming kernel: persistent grid (one wave per workgroup)
 };
 
+// Split-KV partials + combine; picks the streaming kernel (decode_stream.hip)
+// when decode_stream_supported() holds, else the generic one (decode.hip).
 hipError_t launch_decode(const DecodeParams& p, int dtype, bool paged, hipStream_t stream);
+hipError_t launch_decode_combine(const DecodeParams& p, int dtype, bool paged, hipStream_t stream);
+bool decode_stream_supported(int dtype, int head_dim, bool paged, int page_size);
+int decode_stream_waves(int stages, int group);  // resident one-wave workgroups on this device
+int decode_stream_qrows(int group);               // query rows per partial slot
+hipError_t launch_decode_stream(const DecodeParams& p, int dtype, bool paged, hipStream_t stream);
 
 }  // namespace pf
