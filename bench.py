@@ -279,12 +279,16 @@ def cpu_baseline(c3):
 
 
 def load_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch,
+    each scaled by what the counter reads for a 1 GiB copy), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(workload, {}).get(kernel)
+            rec = json.load(f).get(workload, {}).get(kernel)
     except (OSError, ValueError):
         return None
+    return None if rec is None else int(rec["bytes"])
 
 
 def main():
