@@ -109,8 +109,8 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   for (int i = 0; i < NDT; ++i) acc[i] = (f32x16)(0.f);
 
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)G::RB;
-  const rsrc_t krs = make_rsrc(Kb, kv_bytes);
-  const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
+  const i32x4 krs = make_desc(Kb, kv_bytes);
+  const i32x4 vrs = make_desc(Vb, kv_bytes);
   TrAddr<T, D> kta;
   kta.init(lane);
 
@@ -183,6 +183,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   using Frag = typename MF::Frag;
   using G = Tile<T, D>;
   constexpr int BNK = 128, BMQ = 64;
+  constexpr bool kAcc = sizeof(T) == 2;  // dK/dV accumulators in AGPRs
   constexpr int KF = (D / 2) / MF::kK;
   constexpr int NDT = D / 32;
   constexpr int PF = 32 / MF::kK;
@@ -215,7 +216,6 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
     dv[i] = (f32x16)(0.f);
   }
 
-  const bool wave_live = wk0 < p.kv_len;
   const int q_begin = CAUSAL ? (k0 / BMQ) * BMQ : 0;
   const int nqb = (k0 < p.kv_len && q_begin < p.Sq) ? (p.Sq - q_begin + BMQ - 1) / BMQ : 0;
   const int nsteps = nqb * p.g;  // (group member, q block), member-major
@@ -234,21 +234,27 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
     step_coords(st, h, qb0);
     const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
     const uint32_t qbytes = (uint32_t)p.Sq * (uint32_t)G::RB;
-    TileDma<T, D>::load(make_rsrc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, buf, tid);
-    TileDma<T, D>::load(make_rsrc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, buf + G::BYTES, tid);
+    TileDma<T, D>::load(make_desc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, buf, tid);
+    TileDma<T, D>::load(make_desc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, buf + G::BYTES, tid);
+    // Raw load only: a use here would make the wave wait (vmcnt(0)) for the
+    // tile DMA just issued as well; the log2 scaling happens at the store.
     if (tid < 2 * BMQ) {
-      const int q = qb0 + (tid & (BMQ - 1));
-      if (q < p.Sq) lreg = tid < BMQ ? p.lse[qoff + q] * kLog2e : p.delta[qoff + q];
-      else lreg = 0.f;
+      const int q = min(qb0 + (tid & (BMQ - 1)), p.Sq - 1);
+      lreg = (tid < BMQ ? p.lse : p.delta)[qoff + q];
     }
   };
-  auto store_step = [&](char* buf) {
-    if (tid < 2 * BMQ) reinterpret_cast<float*>(buf + 2 * G::BYTES)[tid] = lreg;
+  auto store_step = [&](char* buf, int st) {
+    if (tid < 2 * BMQ) {
+      int h_unused, qb0;
+      step_coords(st, h_unused, qb0);
+      const bool valid = qb0 + (tid & (BMQ - 1)) < p.Sq;
+      reinterpret_cast<float*>(buf + 2 * G::BYTES)[tid] = valid ? (tid < BMQ ? lreg * kLog2e : lreg) : 0.f;
+    }
   };
 
   if (nsteps > 0) {
     load_step(0, smem);
-    store_step(smem);
+    store_step(smem, 0);
   }
   dma_wait();
   __syncthreads();
@@ -265,52 +271,67 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
     char* const nbuf = smem + ((st + 1) & 1) * BUF;
     if (has_next) load_step(st + 1, nbuf);
 
-    if (wave_live && !(CAUSAL && qb0 + BMQ - 1 < wk0)) {
-      f32x16 s0 = (f32x16)(0.f), s1 = (f32x16)(0.f), d0 = (f32x16)(0.f), d1 = (f32x16)(0.f);
-      mfma_nat<T, D>(sq, l32, hh, kf, s0, s1);
-      mfma_nat<T, D>(sdo, l32, hh, vf, d0, d1);
-
-      // lane = key kkey; tile t register r = query qb0 + 32hh + 16t + r.
-      // P overwrites S and dS overwrites dP (mask test hoisted: wave-uniform).
+    {
+      // Every wave runs every step: a step whose keys are all masked for this
+      // wave (past kv_len, or causal rows all above the keys) adds exact zeros
+      // (P = dS = 0), and a branch here would split the dK/dV accumulators'
+      // live ranges across the register files.
+      // lane = key kkey; half t register r = query qb0 + 32hh + 16t + r. The
+      // two 32-query halves run one after the other (S/dP of one half live at
+      // a time), which leaves registers for the LDS reads to run ahead.
       const bool need_mask = (wk0 + 31 >= p.kv_len) || (qb0 + BMQ > p.Sq) || (CAUSAL && qb0 < wk0 + 31);
-      auto softmax_grad = [&](auto masked) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
-          const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
+      auto half = [&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        f32x16 sx = (f32x16)(0.f), dx = (f32x16)(0.f);
+        mfma_nat_pair<T, D>(sq, kf, sdo, vf, t, l32, hh, sx, dx);
+        const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
+        const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
+        // P overwrites S and dS overwrites dP.
+        auto grad = [&](auto masked) {
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
             const f32x4 lv = l4[r4], dl = d4[r4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int r = 4 * r4 + e;
-              const float sx = t ? s1[r] : s0[r];
-              const float dp = t ? d1[r] : d0[r];
-              float pv = __builtin_amdgcn_exp2f(fmaf(sx, p.scale_log2, -lv[e]));
+              float pv = __builtin_amdgcn_exp2f(fmaf(sx[r], p.scale_log2, -lv[e]));
               if constexpr (decltype(masked)::value) {
                 const int q = qb0 + 32 * hh + 16 * t + r;
                 const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
                 pv = ok ? pv : 0.f;
               }
-              const float ds = pv * (dp - dl[e]);
-              if (t) { s1[r] = pv; d1[r] = ds; } else { s0[r] = pv; d0[r] = ds; }
+              dx[r] = pv * (dx[r] - dl[e]);
+              sx[r] = pv;
             }
           }
-        }
+        };
+        if (need_mask) grad(std::true_type{});
+        else grad(std::false_type{});
+        // pack_frags(x, x) puts this half's fragments in both slot ranges;
+        // steps [2t, 2t + 2) read the range of half t.
+        Frag pfr[PF], dsf[PF];
+        pack_frags<T>(sx, sx, pfr);
+        pack_frags<T>(dx, dx, dsf);
+        // dK/dV accumulate in AGPRs (16-bit): the VGPRs stay free for the
+        // S/dP work and for LDS reads issued ahead of their MFMAs.
+        mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sdo, lane, ta, pfr, dv);
+        mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sq, lane, ta, dsf, dk);
       };
-      if (need_mask) softmax_grad(std::true_type{});
-      else softmax_grad(std::false_type{});
-      Frag pfr[PF], dsf[PF];
-      pack_frags<T>(s0, s1, pfr);
-      pack_frags<T>(d0, d1, dsf);
-      mfma_trn<T, D>(sdo, lane, ta, pfr, dv);
-      mfma_trn<T, D>(sq, lane, ta, dsf, dk);
+      half(std::integral_constant<int, 0>{});
+      half(std::integral_constant<int, 1>{});
     }
-    if (has_next) store_step(nbuf);
+    if (has_next) store_step(nbuf, st + 1);
     dma_wait();
     __syncthreads();
   }
 
+  if constexpr (kAcc) {
+#pragma unroll
+    for (int i = 0; i < NDT; ++i) {
+      agpr_fence(dk[i]);
+      agpr_fence(dv[i]);
+    }
+  }
   if (kkey < p.Sk) {
     store_acc_row<T, D>(static_cast<T*>(p.dk) + (koff + kkey) * D, dk, p.sm_scale, hh);
     store_acc_row<T, D>(static_cast<T*>(p.dv) + (koff + kkey) * D, dv, 1.f, hh);

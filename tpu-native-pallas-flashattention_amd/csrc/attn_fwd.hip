@@ -48,6 +48,7 @@ namespace {
 
 constexpr int kFwdBN = 64;   // keys per block
 
+
 template <typename T, int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_attn_fwd_kernel(FwdParams p) {
   using MF = Mfma32<T>;
@@ -87,7 +88,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const int q0 = qblk * p.rpw;
   const int wq0 = q0 + 32 * (wv % wph);
   const int qrow = wq0 + l32;
-  const int wq_last = min(wq0 + 31, p.Sq - 1);
 
   const T* Qb = static_cast<const T*>(p.q) + (int64_t)(b * p.Hq + h) * p.Sq * D;
   const T* Kb = static_cast<const T*>(p.k) + (int64_t)(b * p.Hkv + kvh) * p.Sk * D;
@@ -139,14 +139,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   // ---- staging: K/V rows at or past kv_len lie outside the buffer resources
   // and load as zeros (never read from memory).
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
-  const rsrc_t krs = make_rsrc(Kb, kv_bytes);
-  const rsrc_t vrs = make_rsrc(Vb, kv_bytes);
+  const i32x4 krs = make_desc(Kb, kv_bytes);
+  const i32x4 vrs = make_desc(Vb, kv_bytes);
   // K and V go global -> LDS by DMA (with fused RoPE, p.k is the K rotated
   // once by pf_rope_rotate_k_kernel).
-  auto load_block = [&](int kv0, char* sk, char* sv) {
-    TileDma<T, D>::load(krs, kv0, sk, tid);
-    TileDma<T, D>::load(vrs, kv0, sv, tid);
-  };
 
   float m_run = kNegInf;  // running max, log2 domain (identical in both halves)
   float l_run = 0.f;      // running sum over this lane half's keys
@@ -157,100 +153,147 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   int kv_end = p.kv_len;
   if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + p.rpw, p.Sq));
   const int nblk = (kv_end + BN - 1) / BN;
-  const float c2 = fabsf(p.scale_log2);
+  // c2 = |scale| * log2(e), kept strictly positive so a masked score (-inf)
+  // always gives exp2(-inf * c2 - m) = 0 (sm_scale = 0 then yields the mean of
+  // the valid V rows up to a ~1e-30 relative perturbation of the weights).
+  const float c2 = fmaxf(fabsf(p.scale_log2), 1e-30f);
+  // Valid keys of this lane's query: key < lim (kv_len, and causal key <= q).
+  const int lim = CAUSAL ? min(p.kv_len, qrow + 1) : p.kv_len;
 
   TrAddr<T, D> vta;
   vta.init(lane);
 
-  if (nblk > 0) {
-    load_block(0, smem, smem + G::BYTES);
-  }
-  dma_wait();
-  __syncthreads();
+  // Software pipeline over 64-key blocks, K one block ahead of V:
+  //   iteration j:  S_{j+1} = K_{j+1} Q^T (MFMA)  |  exp / sum / pack of S_j (VALU)
+  //                 O^T += V_j^T P_j^T    (MFMA)  |  masked max of S_{j+1} (VALU)
+  // so each MFMA group has independent VALU work beside it in the same wave.
+  // LDS: kbuf[2] and vbuf[2]; iteration j reads K_{j+1} and V_j while K_{j+2}
+  // (into K_j's buffer) and V_{j+1} (into V_{j-1}'s) stream in.
+  char* const kbuf0 = smem;
+  char* const vbuf0 = smem + 2 * G::BYTES;
+  auto kbuf = [&](int j) { return kbuf0 + (j & 1) * G::BYTES; };
+  auto vbuf = [&](int j) { return vbuf0 + (j & 1) * G::BYTES; };
 
-  for (int j = 0; j < nblk; ++j) {
-    const int kv0 = j * BN;
-    char* const sk = smem + (j & 1) * (2 * G::BYTES);
-    char* const sv = sk + G::BYTES;
-    const bool has_next = j + 1 < nblk;
-    char* const nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
-    if (has_next) load_block(kv0 + BN, nk, nk + G::BYTES);
-
-    const bool live = wq0 < p.Sq && !(CAUSAL && kv0 > wq_last);
-    if (live) {
-      // ---- S^T = K . Q^T --------------------------------------------------
-      f32x16 s[2];
-      s[0] = (f32x16)(0.f);
-      s[1] = (f32x16)(0.f);
-      mfma_nat<T, D>(sk, l32, hh, qf, s[0], s[1]);
-
-      // ---- online softmax (lane owns query qrow; keys kv0 + 32hh + 16t + r)
-      // c2 = |scale| * log2(e) >= 0. The running reference m_run only moves
-      // when some row's max grows by more than 8 (log2 units): p = 2^(x - m)
-      // then stays below 2^8, and since l and acc share the reference the
-      // result is unchanged while the O rescale becomes rare.
-      const bool need_mask = (kv0 + BN > p.kv_len) || (CAUSAL && kv0 + BN - 1 > wq0);
-      float mx = kNegInf;
-      if (need_mask) {
+  // Masked row max of a block's scores (log2 units); masked entries of s
+  // become -inf. lane half hh holds keys kv0 + 32hh + 16t + r.
+  auto block_max = [&](f32x16* s, int kv0) -> float {
+    const int rel = lim - kv0 - 32 * hh;
+    float mx = kNegInf;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + 32 * hh + 16 * t + r;
-            const bool ok = key < p.kv_len && (!CAUSAL || key <= qrow);
-            mx = fmaxf(mx, ok ? s[t][r] : kNegInf);
-          }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+      for (int r = 0; r < 16; ++r) {
+        s[t][r] = (16 * t + r < rel) ? s[t][r] : kNegInf;
+        mx = fmaxf(mx, s[t][r]);
       }
-      mx = wave_xor32_max(mx);
-      mx = (mx == kNegInf) ? kNegInf : mx * c2;
-      const float m_cand = fmaxf(m_run, mx);
-      if (__any(m_cand > m_run + 8.f)) {
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+    return wave_xor32_max(mx) * c2;
+  };
+  // Lazy rescale: the reference m_run only moves when some row's max grows
+  // by more than 8 (log2 units), so p = 2^(x - m) stays below 2^8 and the O
+  // rescale is rare; l and acc share the reference, so o is unchanged.
+  auto update_max = [&](float mx) {
+    const float m_cand = fmaxf(m_run, mx);
+    if (__any(m_cand > m_run + 8.f)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
 #pragma unroll
-        for (int i = 0; i < NDT; ++i) acc[i] *= alpha;
-        l_run *= alpha;
-        m_run = m_cand;
-      }
-      const float m_use = (m_run == kNegInf) ? 0.f : m_run;
-      float rs = 0.f;
-      if (need_mask) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + 32 * hh + 16 * t + r;
-            const bool ok = key < p.kv_len && (!CAUSAL || key <= qrow);
-            const float e = ok ? __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_use)) : 0.f;
-            s[t][r] = e;
-            rs += e;
-          }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float e = __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_use));
-            s[t][r] = e;
-            rs += e;
-          }
-      }
-      l_run += rs;
-
-      // ---- P fragments (B operand of O^T): keys 32hh + m, m = 0..31 --------
-      Frag pfr[PF];
-      pack_frags<T>(s[0], s[1], pfr);
-
-      // ---- O^T += V^T . P^T -------------------------------------------------
-      mfma_trn<T, D>(sv, lane, vta, pfr, acc);
+      for (int i = 0; i < NDT; ++i) acc[i] *= alpha;
+      l_run *= alpha;
+      m_run = m_cand;
     }
+  };
+  // exp2 of a block's (masked) scores against m_run, summed into l_run and
+  // packed as the B operand of O^T += V^T P^T.
+  auto block_exp = [&](f32x16* s, Frag* pfr) {
+    float rs = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[t][r] = __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_run));
+        rs += s[t][r];
+      }
+    l_run += rs;
+    pack_frags<T>(s[0], s[1], pfr);
+  };
+
+  f32x16 s_cur[2];
+  if (nblk > 0) {
+    TileDma<T, D>::load(krs, 0, kbuf(0), tid);
+    TileDma<T, D>::load(vrs, 0, vbuf(0), tid);
+    if (nblk > 1) TileDma<T, D>::load(krs, BN, kbuf(1), tid);
+    dma_wait();
+    __syncthreads();
+    s_cur[0] = (f32x16)(0.f);
+    s_cur[1] = (f32x16)(0.f);
+    mfma_nat<T, D>(kbuf(0), l32, hh, qf, s_cur[0], s_cur[1]);
+    __syncthreads();  // every wave is done with K_0 before K_2 overwrites it
+    update_max(block_max(s_cur, 0));
+  }
+
+  for (int j = 0; j + 1 < nblk; ++j) {
+    const int kv1 = (j + 1) * BN;
+    if (j + 2 < nblk) TileDma<T, D>::load(krs, kv1 + BN, kbuf(j), tid);
+    TileDma<T, D>::load(vrs, kv1, vbuf(j + 1), tid);
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x16 s_nxt[2];
+    s_nxt[0] = (f32x16)(0.f);
+    s_nxt[1] = (f32x16)(0.f);
+    Frag pfr[PF];
+    float mx = kNegInf;
+    if constexpr (sizeof(T) == 2) {
+#ifdef PF_IGLP
+      __builtin_amdgcn_iglp_opt(PF_IGLP);
+#endif
+      // S_{j+1} MFMAs with exp/sum/pack of S_j beside them, then O^T += V_j^T P_j
+      // with the masked max of S_{j+1} beside it (slot = 32 / NV values).
+      constexpr int NV1 = G::CPR, VPS1 = 32 / NV1;
+      constexpr int NV2 = 4 * NDT, VPS2 = 32 / NV2;
+      uint32_t pw[16];
+      float rs = 0.f;
+      mfma_nat_il<T, D>(kbuf(j + 1), l32, hh, qf, s_nxt[0], s_nxt[1], [&](int i) {
+#pragma unroll
+        for (int e = 0; e < VPS1; e += 2) {
+          const int v = i * VPS1 + e;  // value v = tile v / 16, register v % 16
+          const float x0 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][v & 15], c2, -m_run));
+          const float x1 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][(v & 15) + 1], c2, -m_run));
+          rs += x0 + x1;
+          pw[v >> 1] = pack2<T>(x0, x1);
+        }
+      });
+      l_run += rs;
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        pfr[f] = __builtin_bit_cast(Frag, (u32x4){pw[4 * f], pw[4 * f + 1], pw[4 * f + 2], pw[4 * f + 3]});
+      const int rel = lim - kv1 - 32 * hh;
+      mfma_trn_il<T, D>(vbuf(j), vta, pfr, acc, [&](int i) {
+#pragma unroll
+        for (int e = 0; e < VPS2; ++e) {
+          const int v = i * VPS2 + e;
+          const float x = (v < rel) ? s_nxt[v >> 4][v & 15] : kNegInf;
+          s_nxt[v >> 4][v & 15] = x;
+          mx = fmaxf(mx, x);
+        }
+      });
+      mx = wave_xor32_max(mx) * c2;
+    } else {
+      mfma_nat<T, D>(kbuf(j + 1), l32, hh, qf, s_nxt[0], s_nxt[1]);
+      block_exp(s_cur, pfr);
+      mfma_trn<T, D>(vbuf(j), lane, vta, pfr, acc);
+      mx = block_max(s_nxt, kv1);
+    }
+    update_max(mx);
+    s_cur[0] = s_nxt[0];
+    s_cur[1] = s_nxt[1];
 
     dma_wait();
     __syncthreads();
+  }
+
+  if (nblk > 0) {
+    Frag pfr[PF];
+    block_exp(s_cur, pfr);
+    mfma_trn<T, D>(vbuf(nblk - 1), lane, vta, pfr, acc);
   }
 
   // ---- finalize: o = acc / l, lse = m ln2 + ln l ---------------------------

@@ -55,42 +55,9 @@ constexpr int kSK = 32;               // keys per stage
 constexpr int kRowB = 256;            // bytes per K/V row (128 16-bit elements)
 constexpr int kTileB = kSK * kRowB;   // 8 KB: one stage of K (or V)
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline int sswz(int r) { return ((r >> 3) & 1) | ((r & 3) << 1) | (((r >> 4) & 1) << 3); }
-
-// Wave-uniform raw buffer descriptor over [base, base + bytes).
-__device__ inline i32x4 make_desc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  i32x4 d;
-  d[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-  d[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
-  d[2] = __builtin_amdgcn_readfirstlane((int)bytes);
-  d[3] = 0x00020000;
-  return d;
-}
-
-// 64 lanes x 16 bytes: lane l's chunk at byte `voff` of the buffer lands at
-// LDS byte lds_addr + 16 l. Out-of-range lanes write zeros.
-// The compiler's hazard recognizer cannot see inside inline assembly, so the
-// asm pads the two gfx9-family hazards in front of an LDS DMA itself: the
-// descriptor SGPRs come from v_readfirstlane (a VALU write of an SGPR read by
-// a VMEM instruction needs 5 wait states) and the LDS address travels in M0
-// (an SALU write of M0 read by an LDS DMA needs 1). s_nop 4 gives 5.
-__device__ inline void dma_1k(const i32x4& desc, uint32_t voff, uint32_t lds_addr) {
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "{m0}"(lds_addr), "v"(voff), "s"(desc)
-               : "memory");
-}
-
-// Wait until at most N vector-memory loads of this wave are outstanding.
-template <int N>
-__device__ inline void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
 
 // Wait for the oldest issued stage; `younger` later stages (at least 16
 // loads each, loads complete in issue order) may stay in flight.
@@ -103,10 +70,6 @@ __device__ inline void wait_stage(int64_t younger) {
     if (younger >= 1) { wait_vm<16>(); return; }
   }
   wait_vm<0>();
-}
-
-__device__ inline uint32_t lds_u32(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 __device__ inline int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -280,7 +243,7 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < QR / 4; ++i) {
         const int row = 4 * i + h;
-        dma_1k(dq, (uint32_t)(row * kRowB + 16 * (i16 ^ (row & 15))), ldv + kTileB + 1024 * i);
+        dma16(dq, (uint32_t)(row * kRowB + 16 * (i16 ^ (row & 15))), ldv + kTileB + 1024 * i);
       }
     }
     const int kv0 = c.st * kSK;
@@ -290,9 +253,9 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
       const i32x4 dv = make_desc(Vb + seq, (uint32_t)c.L * kRowB);
       const uint32_t rb = (uint32_t)kv0 * kRowB;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dma_1k(dk, rb + loff[i], ldk + 1024 * i);
+      for (int i = 0; i < 8; ++i) dma16(dk, rb + loff[i], ldk + 1024 * i);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dma_1k(dv, rb + loff[i], ldv + 1024 * i);
+      for (int i = 0; i < 8; ++i) dma16(dv, rb + loff[i], ldv + 1024 * i);
     } else {
       const int ps = p.page_size;
       const int64_t trow = (int64_t)c.b * p.pages_per_seq;
@@ -315,9 +278,9 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
         const i32x4 dv = make_desc(Vb + pbase, (uint32_t)(nvalid * kRowB));
         const uint32_t rb = (uint32_t)(kv0 - prow0) * kRowB;
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) dma_1k(dk, rb + loff[gi * kPer + j], ldk + 1024 * (gi * kPer + j));
+        for (int j = 0; j < kPer; ++j) dma16(dk, rb + loff[gi * kPer + j], ldk + 1024 * (gi * kPer + j));
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) dma_1k(dv, rb + loff[gi * kPer + j], ldv + 1024 * (gi * kPer + j));
+        for (int j = 0; j < kPer; ++j) dma16(dv, rb + loff[gi * kPer + j], ldv + 1024 * (gi * kPer + j));
       }
     }
   };

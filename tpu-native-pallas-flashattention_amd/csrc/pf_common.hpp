@@ -153,13 +153,75 @@ __device__ inline u32x4 bufld16(rsrc_t r, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
 }
 
+// Wave-uniform raw buffer descriptor over [base, base + bytes), for the
+// inline-assembly LDS DMA below (base and bytes must be wave-uniform).
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+__device__ inline i32x4 make_desc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 d;
+  d[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  d[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+  d[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  d[3] = 0x00020000;
+  return d;
+}
+
+// Direct global -> LDS load of 64 lanes x 16 bytes (buffer_load_dwordx4 ...
+// lds): lane l's chunk at byte `voff` of the buffer lands at LDS byte
+// lds_addr + 16 l (lds_addr wave-uniform); lanes at or past the descriptor's
+// size write zeros.
+// Issued from inline assembly on purpose: the compiler treats an LDS DMA it
+// can see as a possible alias of every later LDS read and makes the wave wait
+// for all outstanding DMA (vmcnt(0)) before the first such read, which
+// serialises a double-buffered pipeline on the global-load latency. The
+// kernels instead wait explicitly (wait_vm) before the barrier that publishes
+// a DMA'd buffer. The compiler's hazard recognizer cannot see inside inline
+// assembly, so the asm pads the two gfx9-family hazards in front of an LDS
+// DMA itself: the descriptor SGPRs come from v_readfirstlane (a VALU write of
+// an SGPR read by a VMEM instruction needs 5 wait states) and the LDS address
+// travels in M0 (an SALU write of M0 read by an LDS DMA needs 1). s_nop 4
+// gives 5.
+__device__ inline void dma16(const i32x4& desc, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "{m0}"(lds_addr), "v"(voff), "s"(desc)
+               : "memory");
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding
+// (loads complete in issue order).
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+__device__ inline uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 __device__ inline u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void stg16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ inline u32x4 lds16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void sts16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
-__device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
-__device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
+// Reductions over the lane pair (l, l ^ 32) with v_permlane32_swap (a VALU
+// swap of the wave's upper half of one register with the lower half of
+// another): swapping x with itself yields x[l] and x[l ^ 32] in every lane,
+// with no LDS round trip. Both results are symmetric in the pair, and
+// a + b == b + a exactly, so both lane halves get bit-identical values.
+__device__ inline f32x2 lane_pair(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return (f32x2){__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ inline float wave_xor32_max(float x) {
+  const f32x2 v = lane_pair(x);
+  return fmaxf(v[0], v[1]);
+}
+__device__ inline float wave_xor32_sum(float x) {
+  const f32x2 v = lane_pair(x);
+  return v[0] + v[1];
+}
 
 // Workgroup -> work-item remap that keeps the `group` consecutive work items
 // (the query heads of one GQA group) on one XCD. Workgroups are dispatched

@@ -72,31 +72,32 @@ struct TileRegs {
   }
 };
 
-// Direct global -> LDS staging (buffer_load_dwordx4 ... lds): lane l of a
-// wave writes its 16 bytes at the instruction's LDS base (M0) + 16*l, so each
-// lane fetches the global chunk that belongs at its slot of the swizzled
-// tile. No registers hold the data and no LDS store instructions are issued;
-// the issuing wave must wait for vmcnt(0) (dma_wait) before the barrier that
-// publishes the tile.
+// Direct global -> LDS staging (dma16): lane l of a wave writes its 16 bytes
+// at the instruction's LDS base + 16*l, so each lane fetches the global chunk
+// that belongs at its slot of the swizzled tile. No registers hold the data
+// and no LDS store instructions are issued; the issuing wave must wait for
+// its loads (dma_wait) before the barrier that publishes the tile.
 template <typename T, int D>
 struct TileDma {
   using G = Tile<T, D>;
-  __device__ static inline void load(rsrc_t rs, int row0, char* tile, int tid) {
+  __device__ static inline void load(const i32x4& desc, int row0, char* tile, int tid) {
     const int w = tid >> 6, l = tid & 63;
+    const uint32_t lds = lds_u32(tile);
 #pragma unroll
     for (int u = 0; u < G::PER_T; ++u) {
       const int slot = 64 * (4 * u + w) + l;  // 16-byte slot within the tile
       const int row = slot / G::CPR, phys = slot % G::CPR;
       const int chunk = phys ^ tile_swz<G::CPR>(row);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(tile + 16 * 64 * (4 * u + w)), 16,
-          (uint32_t)((row0 + row) * D + chunk * G::EPC) * G::ES, 0, 0, 0);
+      dma16(desc, (uint32_t)((row0 + row) * D + chunk * G::EPC) * G::ES,
+            __builtin_amdgcn_readfirstlane(lds + 16 * 64 * (4 * u + w)));
     }
   }
 };
 
-// Wait for this wave's outstanding global loads (including LDS DMA).
-__device__ inline void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
+// Wait for this wave's outstanding global loads (including LDS DMA). The
+// builtin (vmcnt(0)), not inline assembly, so the compiler's wait tracking
+// knows every earlier load has completed and adds no waits of its own later.
+__device__ inline void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Natural A operand: s0/s1 (32x32 tiles t = 0, 1) += tile rows x B fragments,
 // contracting over D (lane half hh owns columns [hh*D/2, (hh+1)*D/2)).
@@ -170,12 +171,43 @@ struct TrAddr {
   }
 };
 
+// 32x32x16 MFMA whose float32 accumulator lives in AGPRs (inline assembly:
+// the "+a" constraint pins it there, where the allocator would otherwise copy
+// it between the register files around every builtin MFMA once the VGPRs
+// are full). Hazards the compiler cannot see inside the assembly, with the
+// wait states this compiler's own gfx950 hazard model inserts for the
+// builtins: a VALU write of an A/B operand needs 2 before the MFMA reads it
+// (the s_nop 1 below); back-to-back MFMAs accumulating into the same
+// registers need none; an LDS load of an operand is waited for by the
+// compiler (it sees the operand). A VALU/memory read of the result needs 12
+// after the last MFMA: agpr_fence() before the accumulator is read. The
+// statement is not volatile (it touches no memory; data dependencies order
+// it), so the compiler may still hoist LDS reads above it.
+template <typename T>
+struct MfmaAgpr;
+template <>
+struct MfmaAgpr<bf16_t> {
+  __device__ static inline void run(f32x16& acc, bf16x8 a, bf16x8 b) {
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  }
+};
+template <>
+struct MfmaAgpr<f16_t> {
+  __device__ static inline void run(f32x16& acc, f16x8 a, f16x8 b) {
+    asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  }
+};
+// 16 wait states before the compiler may read an AGPR accumulator written by
+// MfmaAgpr (tied to the accumulator so every read is ordered after it).
+__device__ inline void agpr_fence(f32x16& acc) { asm volatile("s_nop 7\n\ts_nop 7" : "+a"(acc)); }
+
 // Transposed A operand: acc[dt] += tile^T (rows = D columns of the tile,
 // reduction over the tile's 64 rows) x B fragments. Lane half hh's B slots
 // for step c are tile rows 32hh + 8c + [0, 8) (16-bit) or 32hh + s (f32).
 // Steps [C0, C1) of 4 (16-bit: step c = tile rows 32hh + 8c + [0, 8); f32:
 // rows 32hh + 8c .. 32hh + 8c + 7 as 8 single-row steps); bf is indexed by step.
-template <typename T, int D, int C0 = 0, int C1 = 4>
+// AGPR = true (16-bit T only): accumulate with MfmaAgpr.
+template <typename T, int D, int C0 = 0, int C1 = 4, bool AGPR = false>
 __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& ta,
                                 const typename Mfma32<T>::Frag* bf, f32x16* acc) {
   using MF = Mfma32<T>;
@@ -195,7 +227,8 @@ __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& 
           part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) v4i16*)(tile + ta.off[dt][r] + (8 * c + 4 * r) * G::RB));
         const Frag af = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
-        acc[dt] = MF::run(af, bf[c], acc[dt]);
+        if constexpr (AGPR) MfmaAgpr<T>::run(acc[dt], af, bf[c]);
+        else acc[dt] = MF::run(af, bf[c], acc[dt]);
       }
   } else {
     const int l32 = lane & 31, hh = lane >> 5;
@@ -211,6 +244,93 @@ __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& 
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Interleaved (software-pipelined) MFMA sequences, 16-bit operands.
+//
+// The same products as mfma_nat / mfma_trn, issued together with a caller
+// VALU stream: valu(i), i = 0 .. NV-1, runs beside the i-th MFMA (NV = number
+// of MFMAs). Each fenced slot (sched_barrier) holds one or two MFMAs, their
+// share of the VALU work and the LDS reads of the MFMAs LEAD slots ahead, so
+// the MFMA pipe and the VALU stay busy together inside one wave and the LDS
+// latency is hidden behind the MFMAs already issued. The VALU work must not
+// depend on the MFMA results of the same sequence.
+// ---------------------------------------------------------------------------
+
+// s0/s1 += tile rows x bf (natural operand, as mfma_nat); NV = CPR (2 per chunk).
+template <typename T, int D, int LEAD = 2, typename VF>
+__device__ inline void mfma_nat_il(const char* tile, int l32, int hh, const typename Mfma32<T>::Frag* bf,
+                                   f32x16& s0, f32x16& s1, VF&& valu) {
+  using MF = Mfma32<T>;
+  using G = Tile<T, D>;
+  static_assert(sizeof(T) == 2, "16-bit operands");
+  constexpr int NC = G::CPR / 2;
+  const int r0 = mfma_src_row(l32, 0), r1 = mfma_src_row(l32, 1);
+  const char* b0 = tile + r0 * G::RB;
+  const char* b1 = tile + r1 * G::RB;
+  const int sw0 = tile_swz<G::CPR>(r0), sw1 = tile_swz<G::CPR>(r1);
+  u32x4 a0[NC], a1[NC];
+#pragma unroll
+  for (int c = 0; c < NC + LEAD; ++c) {
+    if (c < NC) {
+      const int ch = hh * NC + c;
+      a0[c] = lds16(b0 + 16 * (ch ^ sw0));
+      a1[c] = lds16(b1 + 16 * (ch ^ sw1));
+    }
+    if (c >= LEAD) {
+      const int k = c - LEAD;
+      s0 = MF::run(chunk_frag<T>(a0[k], 0), bf[k], s0);
+      valu(2 * k);
+      s1 = MF::run(chunk_frag<T>(a1[k], 0), bf[k], s1);
+      valu(2 * k + 1);
+    }
+#ifndef PF_NO_FENCE
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+  }
+}
+
+// acc[dt] += tile^T x bf (transposed operand, as mfma_trn over all 4 steps);
+// MFMA i = step c * NDT + dt, NV = 4 * NDT.
+template <typename T, int D, int LEAD = 2, typename VF>
+__device__ inline void mfma_trn_il(const char* tile, const TrAddr<T, D>& ta,
+                                   const typename Mfma32<T>::Frag* bf, f32x16* acc, VF&& valu) {
+  using MF = Mfma32<T>;
+  using G = Tile<T, D>;
+  using Frag = typename MF::Frag;
+  static_assert(sizeof(T) == 2, "16-bit operands");
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  constexpr int NDT = D / 32, NM = 4 * NDT;
+  Frag af[NM];
+#pragma unroll
+  for (int i = 0; i < NM + LEAD; ++i) {
+    if (i < NM) {
+      const int c = i / NDT, dt = i % NDT;
+      v4i16 part[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(tile + ta.off[dt][r] + (8 * c + 4 * r) * G::RB));
+      af[i] = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    if (i >= LEAD) {
+      const int k = i - LEAD;
+      acc[k % NDT] = MF::run(af[k], bf[k / NDT], acc[k % NDT]);
+      valu(k);
+    }
+#ifndef PF_NO_FENCE
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+  }
+}
+
+// Two 16-bit values rounded from float32 (round to nearest even), packed low-first.
+template <typename T>
+__device__ inline uint32_t pack2(float a, float b) {
+  typedef T v2 __attribute__((ext_vector_type(2)));
+  const v2 x = {Elem<T>::from_f32(a), Elem<T>::from_f32(b)};
+  return __builtin_bit_cast(uint32_t, x);
 }
 
 // Pack the 32 values a lane holds (tile t register r <-> reduction slot
