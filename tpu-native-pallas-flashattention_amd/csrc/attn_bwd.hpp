@@ -218,16 +218,39 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
 
   const int q_begin = CAUSAL ? (k0 / BMQ) * BMQ : 0;
   const int nqb = (k0 < p.kv_len && q_begin < p.Sq) ? (p.Sq - q_begin + BMQ - 1) / BMQ : 0;
-  const int nsteps = nqb * p.g;  // (group member, q block), member-major
+  const int nsteps = nqb * p.g;  // (group member, q block) pairs
+
+  // Step order: every step that needs a mask for some wave of the workgroup
+  // first, then the rest, so each of the two loops below has one straight-
+  // line body (a branch between masked and unmasked bodies would merge the
+  // dK/dV accumulators across blocks and cost register-file copies).
+  // Masked: the causal diagonal blocks (query block start < k0 + BNK - 1),
+  // the last query block when Sq is ragged, or every block when the
+  // workgroup's keys cross kv_len.
+  const bool all_masked = k0 + BNK > p.kv_len;
+  const int nd = CAUSAL ? min(nqb, (k0 + BNK - 1 - q_begin + BMQ - 1) / BMQ) : 0;
+  const int tail = ((p.Sq - q_begin) % BMQ != 0 && nqb > nd) ? 1 : 0;
+  const int m_pm = all_masked ? nqb : nd + tail;  // masked blocks per member
+  const int u_pm = nqb - m_pm;                     // unmasked blocks per member
+  const int n_masked = m_pm * p.g;
 
   float lreg = 0.f;  // threads 0..63 stage lse, 64..127 stage delta
   TrAddr<T, D> ta;
   ta.init(lane);
 
   auto step_coords = [&](int st, int& h, int& qb0) {
-    const int member = st / nqb;
+    int member, blk;
+    if (st < n_masked) {
+      member = st / m_pm;
+      const int k = st - member * m_pm;
+      blk = (all_masked || k < nd) ? k : nqb - 1;
+    } else {
+      const int jj = st - n_masked;
+      member = jj / u_pm;
+      blk = nd + (jj - member * u_pm);
+    }
     h = kvh * p.g + member;
-    qb0 = q_begin + (st - member * nqb) * BMQ;
+    qb0 = q_begin + blk * BMQ;
   };
   auto load_step = [&](int st, char* buf) {
     int h, qb0;
@@ -259,71 +282,74 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   dma_wait();
   __syncthreads();
 
-  for (int st = 0; st < nsteps; ++st) {
-    const char* buf = smem + (st & 1) * BUF;
-    const char* sq = buf;
-    const char* sdo = buf + G::BYTES;
-    const float* slse = reinterpret_cast<const float*>(buf + 2 * G::BYTES);
-    const float* sdl = slse + BMQ;
-    int h_unused, qb0;
-    step_coords(st, h_unused, qb0);
-    const bool has_next = st + 1 < nsteps;
-    char* const nbuf = smem + ((st + 1) & 1) * BUF;
-    if (has_next) load_step(st + 1, nbuf);
-
-    {
-      // Every wave runs every step: a step whose keys are all masked for this
-      // wave (past kv_len, or causal rows all above the keys) adds exact zeros
-      // (P = dS = 0), and a branch here would split the dK/dV accumulators'
-      // live ranges across the register files.
-      // lane = key kkey; half t register r = query qb0 + 32hh + 16t + r. The
-      // two 32-query halves run one after the other (S/dP of one half live at
-      // a time), which leaves registers for the LDS reads to run ahead.
-      const bool need_mask = (wk0 + 31 >= p.kv_len) || (qb0 + BMQ > p.Sq) || (CAUSAL && qb0 < wk0 + 31);
-      auto half = [&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        f32x16 sx = (f32x16)(0.f), dx = (f32x16)(0.f);
-        mfma_nat_pair<T, D>(sq, kf, sdo, vf, t, l32, hh, sx, dx);
-        const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
-        const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
-        // P overwrites S and dS overwrites dP.
-        auto grad = [&](auto masked) {
+  // One step: lane = key kkey; half t register r = query qb0 + 32hh + 16t + r.
+  // Program order S/dP of both halves, then per half: P, dS (VALU) and
+  // dV^T += dO^T P, dK^T += Q^T dS (MFMA), so the VALU of one half has the
+  // MFMAs of the other in flight beside it. Every wave runs every step: one
+  // whose keys are all masked for it (past kv_len, causal rows all above its
+  // keys) adds exact zeros (P = dS = 0).
+  auto step_body = [&](auto masked, const char* sq, const char* sdo, const float* slse, const float* sdl,
+                       int qb0) {
+    f32x16 sx[2], dx[2];
 #pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            const f32x4 lv = l4[r4], dl = d4[r4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = 4 * r4 + e;
-              float pv = __builtin_amdgcn_exp2f(fmaf(sx[r], p.scale_log2, -lv[e]));
-              if constexpr (decltype(masked)::value) {
-                const int q = qb0 + 32 * hh + 16 * t + r;
-                const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
-                pv = ok ? pv : 0.f;
-              }
-              dx[r] = pv * (dx[r] - dl[e]);
-              sx[r] = pv;
-            }
-          }
-        };
-        if (need_mask) grad(std::true_type{});
-        else grad(std::false_type{});
-        // pack_frags(x, x) puts this half's fragments in both slot ranges;
-        // steps [2t, 2t + 2) read the range of half t.
-        Frag pfr[PF], dsf[PF];
-        pack_frags<T>(sx, sx, pfr);
-        pack_frags<T>(dx, dx, dsf);
-        // dK/dV accumulate in AGPRs (16-bit): the VGPRs stay free for the
-        // S/dP work and for LDS reads issued ahead of their MFMAs.
-        mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sdo, lane, ta, pfr, dv);
-        mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sq, lane, ta, dsf, dk);
-      };
-      half(std::integral_constant<int, 0>{});
-      half(std::integral_constant<int, 1>{});
+    for (int t = 0; t < 2; ++t) {
+      sx[t] = (f32x16)(0.f);
+      dx[t] = (f32x16)(0.f);
+      mfma_nat_pair<T, D>(sq, kf, sdo, vf, t, l32, hh, sx[t], dx[t]);
     }
-    if (has_next) store_step(nbuf, st + 1);
-    dma_wait();
-    __syncthreads();
-  }
+    auto half = [&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
+      const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
+      // P overwrites S and dS overwrites dP.
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x4 lv = l4[r4], dl = d4[r4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lv[e]));
+          if constexpr (decltype(masked)::value) {
+            const int q = qb0 + 32 * hh + 16 * t + r;
+            const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
+            pv = ok ? pv : 0.f;
+          }
+          dx[t][r] = pv * (dx[t][r] - dl[e]);
+          sx[t][r] = pv;
+        }
+      }
+      // pack_frags(x, x) puts this half's fragments in both slot ranges;
+      // steps [2t, 2t + 2) read the range of half t.
+      Frag pfr[PF], dsf[PF];
+      pack_frags<T>(sx[t], sx[t], pfr);
+      pack_frags<T>(dx[t], dx[t], dsf);
+      // dK/dV accumulate in AGPRs (16-bit): the VGPRs stay free for the
+      // S/dP work and for LDS reads issued ahead of their MFMAs.
+      mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sdo, lane, ta, pfr, dv);
+      mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sq, lane, ta, dsf, dk);
+    };
+    half(std::integral_constant<int, 0>{});
+    half(std::integral_constant<int, 1>{});
+  };
+
+  int st = 0;
+  auto run = [&](auto masked, int st_end) {
+    for (; st < st_end; ++st) {
+      const char* buf = smem + (st & 1) * BUF;
+      const float* slse = reinterpret_cast<const float*>(buf + 2 * G::BYTES);
+      int h_unused, qb0;
+      step_coords(st, h_unused, qb0);
+      const bool has_next = st + 1 < nsteps;
+      char* const nbuf = smem + ((st + 1) & 1) * BUF;
+      if (has_next) load_step(st + 1, nbuf);
+      step_body(masked, buf, buf + G::BYTES, slse, slse + BMQ, qb0);
+      if (has_next) store_step(nbuf, st + 1);
+      dma_wait();
+      __syncthreads();
+    }
+  };
+  run(std::true_type{}, n_masked);
+  run(std::false_type{}, nsteps);
 
   if constexpr (kAcc) {
 #pragma unroll
