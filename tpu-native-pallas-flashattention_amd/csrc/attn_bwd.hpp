@@ -90,7 +90,6 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   const int wq0 = q0 + 32 * wv;
   const int qrow = wq0 + l32;
   const bool qvalid = qrow < p.Sq;
-  const int wq_last = min(wq0 + 31, p.Sq - 1);
 
   const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
   const T* Qb = static_cast<const T*>(p.q) + qoff * D;
@@ -125,51 +124,52 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   dma_wait();
   __syncthreads();
 
-  for (int j = 0; j < nblk; ++j) {
+  // Key blocks in two straight-line loops: the leading run that needs no mask
+  // for any wave of the workgroup (below the causal diagonal, inside kv_len,
+  // all rows inside Sq), then the rest (diagonal, kv_len tail) with the mask.
+  // Every wave runs every block: one whose keys are all masked for its rows
+  // adds exact zeros (dS = 0).
+  int n_plain = (q0 + BM > p.Sq) ? 0 : min(nblk, p.kv_len / BN);
+  if constexpr (CAUSAL) n_plain = min(n_plain, q0 / BN);
+
+  auto block = [&](auto masked, int j) {
     const int kv0 = j * BN;
     const char* sk = smem + (j & 1) * (2 * G::BYTES);
     const char* sv = sk + G::BYTES;
-    const bool has_next = j + 1 < nblk;
-    if (has_next) {
+    if (j + 1 < nblk) {
       char* nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
       TileDma<T, D>::load(krs, kv0 + BN, nk, tid);
       TileDma<T, D>::load(vrs, kv0 + BN, nk + G::BYTES, tid);
     }
-    if (wq0 < p.Sq && !(CAUSAL && kv0 > wq_last)) {
-      // keys kv0 + 32hh + 16t + r, query qrow. The two 32-key halves t are
-      // processed one after the other to keep S^T/dP^T register use small.
-      const bool need_mask = (wq0 + 31 >= p.Sq) || (kv0 + BN > p.kv_len) || (CAUSAL && kv0 + BN - 1 > wq0);
-      auto half = [&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        f32x16 sx = (f32x16)(0.f), dx = (f32x16)(0.f);
-        mfma_nat_pair<T, D>(sk, qf, sv, dof, t, l32, hh, sx, dx);
-        if (need_mask) {
+    // keys kv0 + 32hh + 16t + r, query qrow. The two 32-key halves t are
+    // processed one after the other to keep S^T/dP^T register use small.
+    auto half = [&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      f32x16 sx = (f32x16)(0.f), dx = (f32x16)(0.f);
+      mfma_nat_pair<T, D>(sk, qf, sv, dof, t, l32, hh, sx, dx);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + 32 * hh + 16 * t + r;
-            const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
-            const float pv = ok ? __builtin_amdgcn_exp2f(fmaf(sx[r], p.scale_log2, -lse2)) : 0.f;
-            sx[r] = pv * (dx[r] - dlt);
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(sx[r], p.scale_log2, -lse2));
-            sx[r] = pv * (dx[r] - dlt);
-          }
+      for (int r = 0; r < 16; ++r) {
+        float pv = __builtin_amdgcn_exp2f(fmaf(sx[r], p.scale_log2, -lse2));
+        if constexpr (decltype(masked)::value) {
+          const int key = kv0 + 32 * hh + 16 * t + r;
+          const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
+          pv = ok ? pv : 0.f;
         }
-        // pack_frags(x, x) puts this half's fragments in both slot ranges;
-        // steps [2t, 2t + 2) read the range of half t.
-        Frag dsf[PF];
-        pack_frags<T>(sx, sx, dsf);
-        mfma_trn<T, D, 2 * t, 2 * t + 2>(sk, lane, kta, dsf, acc);
-      };
-      half(std::integral_constant<int, 0>{});
-      half(std::integral_constant<int, 1>{});
-    }
+        sx[r] = pv * (dx[r] - dlt);
+      }
+      // pack_frags(x, x) puts this half's fragments in both slot ranges;
+      // steps [2t, 2t + 2) read the range of half t.
+      Frag dsf[PF];
+      pack_frags<T>(sx, sx, dsf);
+      mfma_trn<T, D, 2 * t, 2 * t + 2>(sk, lane, kta, dsf, acc);
+    };
+    half(std::integral_constant<int, 0>{});
+    half(std::integral_constant<int, 1>{});
     dma_wait();
     __syncthreads();
-  }
+  };
+  for (int j = 0; j < n_plain; ++j) block(std::false_type{}, j);
+  for (int j = n_plain; j < nblk; ++j) block(std::true_type{}, j);
 
   if (qvalid) store_acc_row<T, D>(static_cast<T*>(p.dq) + (qoff + qrow) * D, acc, p.sm_scale, hh);
 }

@@ -230,7 +230,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     update_max(block_max(s_cur, 0));
   }
 
-  for (int j = 0; j + 1 < nblk; ++j) {
+  // Iteration j masks block j + 1. Blocks [0, n_plain) need no mask for any
+  // row of the workgroup (below the causal diagonal, inside kv_len), so the
+  // iterations run in two straight-line loops: plain max, then masked max.
+  int n_plain = min(nblk, p.kv_len / BN);
+  if constexpr (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
+
+  auto iter = [&](auto masked, int j) {
     const int kv1 = (j + 1) * BN;
     if (j + 2 < nblk) TileDma<T, D>::load(krs, kv1 + BN, kbuf(j), tid);
     TileDma<T, D>::load(vrs, kv1, vbuf(j + 1), tid);
@@ -242,11 +248,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     Frag pfr[PF];
     float mx = kNegInf;
     if constexpr (sizeof(T) == 2) {
-#ifdef PF_IGLP
-      __builtin_amdgcn_iglp_opt(PF_IGLP);
-#endif
       // S_{j+1} MFMAs with exp/sum/pack of S_j beside them, then O^T += V_j^T P_j
-      // with the masked max of S_{j+1} beside it (slot = 32 / NV values).
+      // with the max of S_{j+1} beside it (slot = 32 / NV values).
       constexpr int NV1 = G::CPR, VPS1 = 32 / NV1;
       constexpr int NV2 = 4 * NDT, VPS2 = 32 / NV2;
       uint32_t pw[16];
@@ -270,8 +273,11 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 #pragma unroll
         for (int e = 0; e < VPS2; ++e) {
           const int v = i * VPS2 + e;
-          const float x = (v < rel) ? s_nxt[v >> 4][v & 15] : kNegInf;
-          s_nxt[v >> 4][v & 15] = x;
+          float x = s_nxt[v >> 4][v & 15];
+          if constexpr (decltype(masked)::value) {
+            x = (v < rel) ? x : kNegInf;
+            s_nxt[v >> 4][v & 15] = x;
+          }
           mx = fmaxf(mx, x);
         }
       });
@@ -288,7 +294,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 
     dma_wait();
     __syncthreads();
-  }
+  };
+  int j = 0;
+  for (; j + 1 < min(n_plain, nblk); ++j) iter(std::false_type{}, j);
+  for (; j + 1 < nblk; ++j) iter(std::true_type{}, j);
 
   if (nblk > 0) {
     Frag pfr[PF];
