@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   const int nsteps = nqb * p.g;  // (group member, q block) pairs
 
   // Step order: every step that needs a mask for some wave of the workgroup
-  // first, then the rest, so each of the two loops below has one straight-
+  // first, then the rest (order below), so each of the two loops has one straight-
   // line body (a branch between masked and unmasked bodies would merge the
   // dK/dV accumulators across blocks and cost register-file copies).
   // Masked: the causal diagonal blocks (query block start < k0 + BNK - 1),
@@ -245,9 +245,14 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       const int k = st - member * m_pm;
       blk = (all_masked || k < nd) ? k : nqb - 1;
     } else {
+      // Unmasked steps: query blocks from the last one down (outer), group
+      // members inner. Workgroups of one (b, kv head) share an XCD and all
+      // start at the top block, so at any time they stream the same Q/dO
+      // tiles and read them mostly from that XCD's L2.
       const int jj = st - n_masked;
-      member = jj / u_pm;
-      blk = nd + (jj - member * u_pm);
+      const int desc = jj / p.g;
+      member = jj - desc * p.g;
+      blk = nd + (u_pm - 1 - desc);
     }
     h = kvh * p.g + member;
     qb0 = q_begin + blk * BMQ;
