@@ -192,6 +192,111 @@ typedef struct {
 size_t pf_paged_attn_workspace_size(const pf_paged_attn_args* args);
 int pf_paged_attn(const pf_paged_attn_args* args, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * KV-cache writes on device. Replaces the decode loop's `_cache_write`
+ * (model.py:257-262, called at :299, :342, :487) and the ring-buffer slot
+ * scatter of prefill_ring (model.py:437, :447-448) / ring_decode_step
+ * (:475-476): rows [0, seq_len) of k/v go to slots pos + i of the contiguous
+ * cache (ring = 0), or to slots (pos + i) mod cache_size (ring = 1; only the
+ * last cache_size rows are written, so no two rows target one slot, which
+ * keeps the tail prefill_ring keeps).
+ *   k, v            [batch, num_kv_heads, seq_len, head_dim]     (dtype)
+ *   k_cache, v_cache [batch, num_kv_heads, cache_size, head_dim] (dtype)
+ *   positions       device int32: absolute position of row 0, read at
+ *                   b * positions_stride (stride 0: one position for all).
+ * A row whose slot is out of range (linear: pos + i outside [0, cache_size);
+ * ring: pos + i < 0) is not written (the reference's dynamic_update_slice
+ * would clamp it onto a valid slot instead).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* k;
+  const void* v;
+  void* k_cache;
+  void* v_cache;
+  const int32_t* positions;
+  int32_t positions_stride;
+  int32_t batch, num_kv_heads, seq_len, cache_size, head_dim;
+  int32_t ring;
+  int32_t dtype;
+} pf_kv_cache_write_args;
+
+int pf_kv_cache_write(const pf_kv_cache_write_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged-pool write (batched). Replaces `write_to_paged_cache`
+ * (paged.py:205-223), which writes one token of one sequence: row i of
+ * sequence b lands at position p = positions[b * positions_stride] + i, i.e.
+ * physical page block_tables[b][p / page_size], offset p % page_size.
+ *   k, v              [batch, num_kv_heads, seq_len, head_dim]          (dtype)
+ *   k_pages, v_pages  [num_pages, num_kv_heads, page_size, head_dim]    (dtype)
+ *   block_tables      [batch, pages_per_seq] int32 (device)
+ * A row is not written when p < 0, its logical page is >= pages_per_seq, or
+ * its table entry lies outside [0, num_pages) (e.g. -1 padding). Rows of
+ * different sequences that map to one (page, offset) race; the caller keeps
+ * them distinct (pages shared between sequences are for read-only prefixes).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* k;
+  const void* v;
+  void* k_pages;
+  void* v_pages;
+  const int32_t* block_tables;
+  const int32_t* positions;
+  int32_t positions_stride;
+  int32_t batch, num_kv_heads, seq_len, num_pages, page_size, head_dim, pages_per_seq;
+  int32_t dtype;
+} pf_paged_cache_write_args;
+
+int pf_paged_cache_write(const pf_paged_cache_write_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused decode step. Replaces the attention part of one decode_step /
+ * ring_decode_step layer (model.py:340-347, :485-491): RoPE of the new
+ * token's q and k at its position (rotate-half, float32, rounded once), the
+ * cache write of k and v at its slot, and single-query attention over the
+ * live slots. Positions live in device memory and no host-side value depends
+ * on them, so one captured step (HIP graph) replays as the caller advances
+ * them on the GPU -- the reference instead re-traces per step because
+ * kv_len is static (flash_attention.py:448).
+ *   q      [batch, num_heads, 1, head_dim]     pre-RoPE (dtype)
+ *   k_new, v_new [batch, num_kv_heads, 1, head_dim]  k pre-RoPE (dtype)
+ *   k_cache, v_cache [batch, num_kv_heads, cache_size, head_dim]
+ *   o      [batch, num_heads, 1, head_dim]
+ *   positions  device int32, read at b * positions_stride
+ *   cos, sin   [rope_len, head_dim] float32 (precompute_rope), or both NULL
+ *              for no rotation
+ *   ring = 0: slot pos, attends slots [0, pos] (valid iff 0 <= pos < cache_size)
+ *   ring = 1: slot pos % cache_size, attends min(pos + 1, cache_size) slots
+ *             (valid iff pos >= 0); model.py:475-476
+ * With RoPE, a valid position is also < rope_len. An invalid position writes
+ * nothing and gives o = 0 for that batch.
+ * Supported: bf16 / f16 with head_dim 128 (PF_ERR_UNSUPPORTED otherwise).
+ * workspace: at least pf_attn_decode_step_workspace_size(args) bytes,
+ * 256-byte aligned (contents on entry do not matter).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* q;
+  const void* k_new;
+  const void* v_new;
+  void* k_cache;
+  void* v_cache;
+  void* o;
+  const int32_t* positions;
+  int32_t positions_stride;
+  const float* cos;
+  const float* sin;
+  int32_t rope_len;
+  int32_t batch, num_heads, num_kv_heads, cache_size, head_dim;
+  int32_t ring;
+  float sm_scale;
+  int32_t dtype;
+  void* workspace;
+  size_t workspace_bytes;
+} pf_attn_decode_step_args;
+
+size_t pf_attn_decode_step_workspace_size(const pf_attn_decode_step_args* args);
+int pf_attn_decode_step(const pf_attn_decode_step_args* args, void* stream);
+
 /* Library version string (static storage). */
 const char* pf_version(void);
 

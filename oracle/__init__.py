@@ -24,5 +24,8 @@ from .attention import (  # noqa: F401
     decode_ref,
     paged_ref,
     gather_pages_ref,
+    cache_write_ref,
+    paged_write_ref,
+    decode_step_ref,
     brute_force_attention,
 )

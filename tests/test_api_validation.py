@@ -116,3 +116,55 @@ def test_paged_validation(case):
         lens = torch.tensor([5], dtype=torch.int32)
     with pytest.raises(ValueError):
         paged_flash_attention(q, kp, vp, table, lens)
+
+
+# ------------------------------------------------ decode-loop primitives --
+from pallas_flash import flash_attention_decode_step, ring_kv_len, write_kv_cache  # noqa: E402
+
+
+def test_ring_kv_len_matches_reference():
+    # test_streaming.py:28-32
+    assert ring_kv_len(3, 8) == 3
+    assert ring_kv_len(8, 8) == 8
+    assert ring_kv_len(50, 8) == 8
+    assert ring_kv_len(1, 8) == 1
+
+
+def test_decode_step_validation_before_device():
+    z = lambda *s: torch.zeros(s)
+    q, kn, vn, kc, vc = z(2, 8, 1, 128), z(2, 2, 1, 128), z(2, 2, 1, 128), z(2, 2, 64, 128), z(2, 2, 64, 128)
+    with pytest.raises(ValueError):
+        flash_attention_decode_step(z(2, 8, 2, 128), kn, vn, kc, vc, 0)        # two query rows
+    with pytest.raises(ValueError):
+        flash_attention_decode_step(q, z(2, 2, 2, 128), vn, kc, vc, 0)          # k_new rows
+    with pytest.raises(ValueError):
+        flash_attention_decode_step(z(2, 6, 1, 128), kn, vn, z(2, 4, 64, 128), z(2, 4, 64, 128), 0)
+    with pytest.raises(ValueError):
+        flash_attention_decode_step(q, kn, vn, kc, vc, 0, cos=z(64, 128))       # sin missing
+    with pytest.raises(ValueError):
+        flash_attention_decode_step(q, kn, vn, kc, vc, [0, 1, 2])               # 3 positions for batch 2
+    with pytest.raises(ValueError):
+        flash_attention_decode_step(q, kn, vn, kc, vc, torch.tensor([0.5, 1.0]))
+    with pytest.raises(RuntimeError):                                           # valid, but no device path
+        flash_attention_decode_step(q, kn, vn, kc, vc, 0)
+
+
+def test_write_kv_cache_validation_before_device():
+    z = lambda *s: torch.zeros(s)
+    with pytest.raises(ValueError):
+        write_kv_cache(z(2, 2, 8, 64), z(2, 2, 8, 64), z(2, 3, 1, 64), z(2, 3, 1, 64), 0)
+    with pytest.raises(ValueError):
+        write_kv_cache(z(2, 2, 8, 64), z(2, 2, 9, 64), z(2, 2, 1, 64), z(2, 2, 1, 64), 0)
+    with pytest.raises(RuntimeError):
+        write_kv_cache(z(2, 2, 8, 64), z(2, 2, 8, 64), z(2, 2, 1, 64), z(2, 2, 1, 64), 0)
+
+
+def test_write_to_paged_cache_validation_before_device():
+    from pallas_flash import write_to_paged_cache
+    z = lambda *s: torch.zeros(s)
+    with pytest.raises(ValueError):   # table rows != batch
+        write_to_paged_cache(z(4, 2, 16, 64), z(4, 2, 16, 64), z(2, 2, 1, 64), z(2, 2, 1, 64),
+                             torch.zeros(3, 4, dtype=torch.int32), 0)
+    with pytest.raises(RuntimeError):
+        write_to_paged_cache(z(4, 2, 16, 64), z(4, 2, 16, 64), z(1, 2, 1, 64), z(1, 2, 1, 64),
+                             torch.zeros(4, dtype=torch.int32), 0)

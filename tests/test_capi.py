@@ -35,7 +35,8 @@ def test_header_declares_expected_entry_points():
                  "pf_attn_bwd", "pf_attn_bwd_delta",
                  "pf_attn_bwd_dq", "pf_attn_bwd_dkv", "pf_attn_decode",
                  "pf_attn_decode_workspace_size", "pf_paged_attn", "pf_paged_attn_workspace_size",
-                 "pf_version"):
+                 "pf_kv_cache_write", "pf_paged_cache_write", "pf_attn_decode_step",
+                 "pf_attn_decode_step_workspace_size", "pf_version"):
         assert want in names
 
 
@@ -56,6 +57,12 @@ def test_struct_sizes_match_c_layout():
     assert ctypes.sizeof(_lib.BwdArgs) == 10 * 8 + 10 * 4
     assert ctypes.sizeof(_lib.DecodeArgs) == 4 * 8 + 8 * 4 + 8 + 8
     assert ctypes.sizeof(_lib.PagedArgs) == 6 * 8 + 9 * 4 + 4 + 8 + 8
+    assert ctypes.sizeof(_lib.KvWriteArgs) == 5 * 8 + 8 * 4
+    assert ctypes.sizeof(_lib.PagedWriteArgs) == 6 * 8 + 9 * 4 + 4
+    # 7 pointers, stride + pad, cos/sin, 9 x 4-byte fields + pad, workspace, size_t
+    assert ctypes.sizeof(_lib.DecodeStepArgs) == 7 * 8 + 8 + 2 * 8 + 9 * 4 + 4 + 8 + 8
+    assert _lib.DecodeStepArgs.cos.offset == 7 * 8 + 8
+    assert _lib.DecodeStepArgs.workspace.offset == 7 * 8 + 8 + 2 * 8 + 9 * 4 + 4
 
 
 def _fwd(**over):
@@ -157,3 +164,75 @@ def test_status_mapping():
         _lib.check(_lib.PF_ERR_UNSUPPORTED, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.PF_ERR_LAUNCH, "x")
+
+
+def _kvw(**over):
+    base = dict(k=8, v=8, k_cache=8, v_cache=8, positions=8, positions_stride=1, batch=2,
+                num_kv_heads=2, seq_len=3, cache_size=16, head_dim=128, ring=0, dtype=1)
+    base.update(over)
+    return _lib.KvWriteArgs(**base)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(batch=-1), _lib.PF_ERR_INVALID),
+    (dict(positions_stride=2), _lib.PF_ERR_INVALID),
+    (dict(ring=3), _lib.PF_ERR_INVALID),
+    (dict(cache_size=0), _lib.PF_ERR_INVALID),
+    (dict(positions=None), _lib.PF_ERR_INVALID),
+    (dict(dtype=9), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=96), _lib.PF_ERR_UNSUPPORTED),
+    (dict(seq_len=0, k=None, v=None, positions=None), _lib.PF_OK),  # nothing to write
+])
+def test_kv_cache_write_rejects_on_host(L, over, status):
+    assert L.pf_kv_cache_write(_kvw(**over), None) == status
+
+
+def _pw(**over):
+    base = dict(k=8, v=8, k_pages=8, v_pages=8, block_tables=8, positions=8, positions_stride=0,
+                batch=2, num_kv_heads=2, seq_len=1, num_pages=10, page_size=16, head_dim=128,
+                pages_per_seq=4, dtype=1)
+    base.update(over)
+    return _lib.PagedWriteArgs(**base)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(num_pages=0), _lib.PF_ERR_INVALID),
+    (dict(page_size=0), _lib.PF_ERR_INVALID),
+    (dict(pages_per_seq=-1), _lib.PF_ERR_INVALID),
+    (dict(block_tables=None), _lib.PF_ERR_INVALID),
+    (dict(positions_stride=5), _lib.PF_ERR_INVALID),
+    (dict(dtype=4), _lib.PF_ERR_UNSUPPORTED),
+    (dict(pages_per_seq=0, block_tables=None), _lib.PF_OK),  # no page to write into
+])
+def test_paged_cache_write_rejects_on_host(L, over, status):
+    assert L.pf_paged_cache_write(_pw(**over), None) == status
+
+
+def _step(**over):
+    base = dict(q=8, k_new=8, v_new=8, k_cache=8, v_cache=8, o=8, positions=8, positions_stride=1,
+                cos=8, sin=8, rope_len=8192, batch=64, num_heads=32, num_kv_heads=8, cache_size=8192,
+                head_dim=128, ring=0, sm_scale=0.1, dtype=1, workspace=None, workspace_bytes=0)
+    base.update(over)
+    return _lib.DecodeStepArgs(**base)
+
+
+def test_decode_step_workspace_and_rejections(L):
+    ws = L.pf_attn_decode_step_workspace_size(_step())
+    assert ws > 0 and ws % 256 == 0
+    # rotated q (64 x 32 x 128 bf16) + lengths + decode partials
+    assert ws >= 64 * 32 * 128 * 2 + 256
+    assert L.pf_attn_decode_step(_step(), None) == _lib.PF_ERR_WORKSPACE
+    assert L.pf_attn_decode_step(_step(workspace=256, workspace_bytes=ws - 1), None) == _lib.PF_ERR_WORKSPACE
+    assert L.pf_attn_decode_step(_step(workspace=100, workspace_bytes=ws), None) == _lib.PF_ERR_WORKSPACE
+    for over, status in [(dict(sin=None), _lib.PF_ERR_INVALID),       # tables come in pairs
+                         (dict(rope_len=0), _lib.PF_ERR_INVALID),
+                         (dict(num_heads=12), _lib.PF_ERR_INVALID),
+                         (dict(positions_stride=2), _lib.PF_ERR_INVALID),
+                         (dict(ring=2), _lib.PF_ERR_INVALID),
+                         (dict(sm_scale=float("inf")), _lib.PF_ERR_INVALID),
+                         (dict(dtype=0), _lib.PF_ERR_UNSUPPORTED),     # streaming path: 16-bit only
+                         (dict(head_dim=64), _lib.PF_ERR_UNSUPPORTED)]:
+        assert L.pf_attn_decode_step(_step(**over), None) == status, over
+        assert L.pf_attn_decode_step_workspace_size(_step(**over)) == 0, over
+    # no tables: no rotation, still valid
+    assert L.pf_attn_decode_step_workspace_size(_step(cos=None, sin=None, rope_len=0)) == ws

@@ -335,3 +335,120 @@ def test_gather_never_reads_past_live_pages():
     pages = np.arange(4 * 1 * 2 * 1, dtype=float).reshape(4, 1, 2, 1)
     g = gather_pages_ref(pages, np.array([2, -1, -1]), 2)
     np.testing.assert_array_equal(g[0, :, 0], [4.0, 5.0])
+
+
+# ------------------------------------------- decode-loop cache primitives --
+from oracle import cache_write_ref, decode_step_ref, paged_write_ref  # noqa: E402
+
+
+def test_cache_write_linear_is_slice_assignment(rng):
+    cache = rng.standard_normal((2, 3, 10, 4))
+    rows = rng.standard_normal((2, 3, 4, 4))
+    got = cache_write_ref(cache, rows, [2, 8])
+    want = cache.copy()
+    want[0, :, 2:6] = rows[0]          # fits
+    want[1, :, 8:10] = rows[1, :, :2]  # rows past the capacity are dropped
+    assert np.array_equal(got, want)
+
+
+def test_cache_write_ring_batch_equals_one_at_a_time(rng):
+    C, S = 6, 15
+    cache = rng.standard_normal((1, 2, C, 3))
+    rows = rng.standard_normal((1, 2, S, 3))
+    at_once = cache_write_ref(cache, rows, 0, ring=True)
+    seq = cache.copy()
+    for i in range(S):
+        seq = cache_write_ref(seq, rows[:, :, i:i + 1], i, ring=True)
+    assert np.array_equal(at_once, seq)
+    # the ring holds the last C tokens, token p at slot p % C (np.roll of the window)
+    window = rows[0, :, S - C:]
+    assert np.array_equal(at_once[0], np.roll(window, (S - C) % C, axis=1))
+
+
+def test_paged_write_then_gather_round_trip(rng):
+    num_pages, page = 9, 4
+    pool = np.full((num_pages, 2, page, 3), np.nan)
+    table = np.array([[5, 1, 7, -1], [2, 0, -1, -1]])
+    lens = [11, 6]
+    rows = rng.standard_normal((2, 2, 11, 3))
+    out = pool
+    for b in range(2):
+        out = paged_write_ref(out, rows[b:b + 1, :, :lens[b]], table[b:b + 1], 0)
+    for b in range(2):
+        assert np.array_equal(gather_pages_ref(out, table[b], lens[b]), rows[b, :, :lens[b]])
+    # pages no live token maps to stay untouched (NaN); -1 entries are never written
+    untouched = [p for p in range(num_pages) if p not in (5, 1, 7, 2, 0)]
+    assert np.isnan(out[untouched]).all()
+    # a write past the table or through -1 padding is dropped
+    again = paged_write_ref(out, rows[1:2, :, :1], table[1:2], 9)  # logical page 2 -> -1
+    assert np.array_equal(np.nan_to_num(again, nan=7.0), np.nan_to_num(out, nan=7.0))
+
+
+def _decode_problem(rng, B, Hq, Hkv, C, D):
+    q = rng.standard_normal((B, Hq, 1, D))
+    kn = rng.standard_normal((B, Hkv, 1, D))
+    vn = rng.standard_normal((B, Hkv, 1, D))
+    kc = rng.standard_normal((B, Hkv, C, D))
+    vc = rng.standard_normal((B, Hkv, C, D))
+    return q, kn, vn, kc, vc
+
+
+def test_decode_step_equals_decode_on_built_cache(rng):
+    B, Hq, Hkv, C, D = 2, 4, 2, 12, 8
+    q, kn, vn, kc, vc = _decode_problem(rng, B, Hq, Hkv, C, D)
+    pos = [5, 11]
+    o, kc2, vc2 = decode_step_ref(q, kn, vn, kc, vc, pos)
+    for b in range(B):
+        kb, vb = kc.copy(), vc.copy()
+        kb[b, :, pos[b]] = kn[b, :, 0]
+        vb[b, :, pos[b]] = vn[b, :, 0]
+        assert np.array_equal(kc2[b], kb[b]) and np.array_equal(vc2[b], vb[b])
+        ref = decode_ref(q[b:b + 1], kb[b:b + 1], vb[b:b + 1], pos[b] + 1)
+        np.testing.assert_allclose(o[b], ref[0], rtol=0, atol=1e-12)
+    # invalid positions: nothing written, o = 0
+    o_bad, kc3, _ = decode_step_ref(q, kn, vn, kc, vc, [-1, C])
+    assert not o_bad.any() and np.array_equal(kc3, kc)
+
+
+def test_decode_step_ring_equals_window_in_order(rng):
+    """test_streaming.py:82-103: a wrapped ring gives attention over the window."""
+    B, Hq, Hkv, C, D, T = 1, 2, 2, 8, 8, 21
+    toks_k = rng.standard_normal((B, Hkv, T, D))
+    toks_v = rng.standard_normal((B, Hkv, T, D))
+    q = rng.standard_normal((B, Hq, 1, D))
+    kc = np.zeros((B, Hkv, C, D))
+    vc = np.zeros((B, Hkv, C, D))
+    for p in range(T - 1):
+        kc = cache_write_ref(kc, toks_k[:, :, p:p + 1], p, ring=True)
+        vc = cache_write_ref(vc, toks_v[:, :, p:p + 1], p, ring=True)
+    o, _, _ = decode_step_ref(q, toks_k[:, :, T - 1:], toks_v[:, :, T - 1:], kc, vc, T - 1, ring=True)
+    window_o, _ = attention_ref(q, toks_k[:, :, T - C:], toks_v[:, :, T - C:])
+    np.testing.assert_allclose(o, window_o, rtol=0, atol=1e-12)
+
+
+def test_decode_step_rope_relative_position_invariance(rng):
+    """Shifting every position by a constant leaves o unchanged once the ring
+    has wrapped (every slot live; scores <R_m q, R_n k> depend on m - n and
+    attention ignores slot order); position 0 is the unrotated problem."""
+    B, Hq, Hkv, C, D, T = 1, 2, 1, 16, 8, 20
+    cos, sin = precompute_rope_ref(64, D)
+    ks = rng.standard_normal((B, Hkv, T, D))
+    vs = rng.standard_normal((B, Hkv, T, D))
+    q = rng.standard_normal((B, Hq, 1, D))
+
+    def run(shift):
+        kc = np.zeros((B, Hkv, C, D))
+        vc = np.zeros((B, Hkv, C, D))
+        o = None
+        for t in range(T):
+            o, kc, vc = decode_step_ref(q, ks[:, :, t:t + 1], vs[:, :, t:t + 1], kc, vc, t + shift,
+                                        cos, sin, ring=True)
+        return o
+
+    np.testing.assert_allclose(run(0), run(7), rtol=0, atol=1e-10)
+    # position 0, single token: rotation is the identity (cos = 1, sin = 0)
+    q0, kn, vn, kc, vc = _decode_problem(rng, 1, 2, 1, 4, D)
+    o_rot, kc_rot, _ = decode_step_ref(q0, kn, vn, kc, vc, 0, cos, sin)
+    o_plain, kc_plain, _ = decode_step_ref(q0, kn, vn, kc, vc, 0)
+    np.testing.assert_allclose(o_rot, o_plain, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(kc_rot, kc_plain, rtol=0, atol=1e-12)

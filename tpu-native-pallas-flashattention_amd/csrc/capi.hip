@@ -355,4 +355,102 @@ int pf_paged_attn(const pf_paged_attn_args* a, void* stream) {
   return finish(pf::launch_decode(p, a->dtype, true, (hipStream_t)stream));
 }
 
+// ---------------------------------------------------------------------------
+// Cache writes and the fused decode step
+// ---------------------------------------------------------------------------
+int pf_kv_cache_write(const pf_kv_cache_write_args* a, void* stream) {
+  if (!a) return PF_ERR_INVALID;
+  if (a->batch < 0 || a->num_kv_heads < 1 || a->seq_len < 0 || a->cache_size < 1) return PF_ERR_INVALID;
+  if (a->positions_stride != 0 && a->positions_stride != 1) return PF_ERR_INVALID;
+  if (a->ring != 0 && a->ring != 1) return PF_ERR_INVALID;
+  if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if ((int64_t)a->batch * a->num_kv_heads * a->seq_len == 0) return PF_OK;
+  if (!a->k || !a->v || !a->k_cache || !a->v_cache || !a->positions) return PF_ERR_INVALID;
+  pf::KvWriteParams p{a->k, a->v, a->k_cache, a->v_cache, a->positions, a->positions_stride,
+                      a->batch, a->num_kv_heads, a->seq_len, a->cache_size, a->ring};
+  return finish(pf::launch_kv_cache_write(p, a->dtype, a->head_dim, (hipStream_t)stream));
+}
+
+int pf_paged_cache_write(const pf_paged_cache_write_args* a, void* stream) {
+  if (!a) return PF_ERR_INVALID;
+  if (a->batch < 0 || a->num_kv_heads < 1 || a->seq_len < 0 || a->num_pages < 1 || a->page_size < 1 ||
+      a->pages_per_seq < 0)
+    return PF_ERR_INVALID;
+  if (a->positions_stride != 0 && a->positions_stride != 1) return PF_ERR_INVALID;
+  if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if ((int64_t)a->batch * a->num_kv_heads * a->seq_len == 0 || a->pages_per_seq == 0) return PF_OK;
+  if (!a->k || !a->v || !a->k_pages || !a->v_pages || !a->positions || !a->block_tables) return PF_ERR_INVALID;
+  pf::PagedWriteParams p{a->k, a->v, a->k_pages, a->v_pages, a->block_tables, a->positions,
+                         a->positions_stride, a->batch, a->num_kv_heads, a->seq_len, a->num_pages,
+                         a->page_size, a->pages_per_seq};
+  return finish(pf::launch_paged_cache_write(p, a->dtype, a->head_dim, (hipStream_t)stream));
+}
+
+// Workspace of the decode step: rotated queries, per-batch live lengths, then
+// the streaming decode's partials.
+static int fill_decode_step(const pf_attn_decode_step_args* a, pf::DecodeParams* p, size_t* q_bytes,
+                            size_t* len_bytes) {
+  if (!a) return PF_ERR_INVALID;
+  if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->cache_size < 1) return PF_ERR_INVALID;
+  if (a->num_heads % a->num_kv_heads != 0) return PF_ERR_INVALID;
+  if (a->positions_stride != 0 && a->positions_stride != 1) return PF_ERR_INVALID;
+  if (a->ring != 0 && a->ring != 1) return PF_ERR_INVALID;
+  if ((a->cos == nullptr) != (a->sin == nullptr)) return PF_ERR_INVALID;
+  if (a->cos != nullptr && a->rope_len < 1) return PF_ERR_INVALID;
+  if (!isfinite(a->sm_scale)) return PF_ERR_INVALID;
+  if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
+  if (!pf::decode_stream_supported(a->dtype, a->head_dim, false, 0)) return PF_ERR_UNSUPPORTED;
+  if ((int64_t)a->cache_size * a->head_dim * 2 >= ((int64_t)1 << 31)) return PF_ERR_UNSUPPORTED;
+  *p = pf::DecodeParams{};
+  p->k = a->k_cache;
+  p->v = a->v_cache;
+  p->o = a->o;
+  p->B = a->batch;
+  p->Hq = a->num_heads;
+  p->Hkv = a->num_kv_heads;
+  p->D = a->head_dim;
+  p->cache_size = a->cache_size;
+  p->cache_len = a->cache_size;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  if (stream_setup(p, a->num_heads / a->num_kv_heads) <= 0) return PF_ERR_LAUNCH;
+  *q_bytes = align256((size_t)a->batch * a->num_heads * a->head_dim * 2);
+  *len_bytes = align256((size_t)a->batch * sizeof(int32_t));
+  return PF_OK;
+}
+
+size_t pf_attn_decode_step_workspace_size(const pf_attn_decode_step_args* a) {
+  pf::DecodeParams p;
+  size_t qb = 0, lb = 0;
+  if (fill_decode_step(a, &p, &qb, &lb) != PF_OK) return 0;
+  return qb + lb + decode_ws_bytes(p);
+}
+
+int pf_attn_decode_step(const pf_attn_decode_step_args* a, void* stream) {
+  pf::DecodeParams p;
+  size_t qb = 0, lb = 0;
+  int st = fill_decode_step(a, &p, &qb, &lb);
+  if (st != PF_OK) return st;
+  if (a->batch == 0) return PF_OK;
+  if (!a->q || !a->k_new || !a->v_new || !a->k_cache || !a->v_cache || !a->o || !a->positions)
+    return PF_ERR_INVALID;
+  const size_t need = qb + lb + decode_ws_bytes(p);
+  if (!a->workspace || a->workspace_bytes < need || ((uintptr_t)a->workspace & 255) != 0)
+    return PF_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(a->workspace);
+  pf::DecodeStepParams sp{a->q, a->k_new, a->v_new, a->k_cache, a->v_cache, ws,
+                          reinterpret_cast<int32_t*>(ws + qb), a->positions, a->positions_stride,
+                          a->cos, a->sin, a->rope_len, a->batch, a->num_heads, a->num_kv_heads,
+                          a->cache_size, a->ring};
+  st = bind_workspace(&p, ws + qb + lb, a->workspace_bytes - qb - lb);
+  if (st != PF_OK) return st;
+  p.q = ws;                                            // rotated queries
+  p.context_lens = reinterpret_cast<int32_t*>(ws + qb);  // device-side live lengths
+  const hipStream_t s = (hipStream_t)stream;
+  st = finish(pf::launch_decode_step_prep(sp, a->dtype, a->head_dim, s));
+  if (st != PF_OK) return st;
+  return finish(pf::launch_decode(p, a->dtype, false, s));
+}
+
 }  // extern "C"

@@ -104,11 +104,18 @@ struct Mfma16<f16_t> {
   }
 };
 
+// Clamp of a device-side length: contiguous cache (PG == 1) to its capacity,
+// paged pool to the table's reach.
+template <int PG>
+__device__ inline int clamp_len(const DecodeParams& p, int raw) {
+  return min(max(raw, 0), PG == 1 ? p.cache_size : p.pages_per_seq * p.page_size);
+}
+
 // Valid keys of batch b.
 template <int PG>
 __device__ inline int seq_len(const DecodeParams& p, int b) {
   if constexpr (PG != 0) {
-    return min(max(sload_i32(p.context_lens, b), 0), p.pages_per_seq * p.page_size);
+    return clamp_len<PG>(p, sload_i32(p.context_lens, b));
   } else {
     return p.cache_len;
   }
@@ -162,7 +169,7 @@ __device__ inline int64_t locate(const DecodeParams& p, int J, int64_t s, Cursor
     int64_t base = 0;
     for (int b0 = 0; b0 < p.B; b0 += 64) {
       const int bb = b0 + lane;
-      const int Lb = bb < p.B ? min(max(p.context_lens[bb], 0), p.pages_per_seq * p.page_size) : 0;
+      const int Lb = bb < p.B ? clamp_len<PG>(p, p.context_lens[bb]) : 0;
       const int64_t t = (int64_t)((Lb + kSK - 1) / kSK) * J;
       int64_t incl = t;  // inclusive scan over the 64 lanes
 #pragma unroll
@@ -187,8 +194,10 @@ __device__ inline int64_t locate(const DecodeParams& p, int J, int64_t s, Cursor
   }
 }
 
-// PG: 0 = contiguous cache; 32 = paged with page_size % 32 == 0 (one page
-// per stage); 4 = paged with page_size % 4 == 0 (one page per 4-row load).
+// PG: 0 = contiguous cache, one length (cache_len) for every batch; 1 =
+// contiguous cache, per-batch lengths in device memory (context_lens, as the
+// fused decode step writes them); 32 = paged with page_size % 32 == 0 (one
+// page per stage); 4 = paged with page_size % 4 == 0 (one page per 4-row load).
 // QR: query rows staged per sequence (4 when the group has <= 4 heads, else 16).
 template <typename T, int PG, int NS, int QR>
 __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
@@ -247,7 +256,7 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
       }
     }
     const int kv0 = c.st * kSK;
-    if constexpr (PG == 0) {
+    if constexpr (PG == 0 || PG == 1) {
       const int64_t seq = ((int64_t)c.b * p.Hkv + kvh) * (int64_t)p.cache_size * 128;
       const i32x4 dk = make_desc(Kb + seq, (uint32_t)c.L * kRowB);
       const i32x4 dv = make_desc(Vb + seq, (uint32_t)c.L * kRowB);
@@ -455,13 +464,13 @@ __global__ __launch_bounds__(256) void pf_decode_stream_combine_kernel(DecodePar
   } else {
     for (int b0 = 0; b0 < b; b0 += 64) {
       const int bb = b0 + lane;
-      const int Lb = bb < b ? min(max(p.context_lens[bb], 0), p.pages_per_seq * p.page_size) : 0;
+      const int Lb = bb < b ? clamp_len<PG>(p, p.context_lens[bb]) : 0;
       int64_t t = (int64_t)((Lb + kSK - 1) / kSK) * J;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
       before += t;
     }
-    L = min(max(p.context_lens[b], 0), p.pages_per_seq * p.page_size);
+    L = clamp_len<PG>(p, p.context_lens[b]);
   }
   const int nst = (L + kSK - 1) / kSK;
   T* out = static_cast<T*>(p.o) + (int64_t)bh * 128 + 2 * lane;
@@ -521,7 +530,7 @@ hipError_t launch_qr(const DecodeParams& p, hipStream_t st) {
 
 template <typename T>
 hipError_t launch_pg(const DecodeParams& p, bool paged, hipStream_t st) {
-  if (!paged) return launch_qr<T, 0>(p, st);
+  if (!paged) return p.context_lens != nullptr ? launch_qr<T, 1>(p, st) : launch_qr<T, 0>(p, st);
   if (p.page_size % 32 == 0) return launch_qr<T, 32>(p, st);
   return launch_qr<T, 4>(p, st);
 }

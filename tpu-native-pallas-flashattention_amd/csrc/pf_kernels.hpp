@@ -63,7 +63,8 @@ struct DecodeParams {
   const void* v;
   void* o;
   const int32_t* block_tables;  // null for the contiguous cache
-  const int32_t* context_lens;  // null for the contiguous cache
+  const int32_t* context_lens;  // paged: [B] lengths; contiguous: null (cache_len
+                                // for every batch) or [B] lengths in device memory
   float* part_o;                // [B, Hq, n_split, D] partial (unnormalised) outputs
   float* part_ml;               // [B, Hq, n_split, 2] partial (max, sum)
   int B, Hq, Hkv, D;
@@ -85,5 +86,52 @@ bool decode_stream_supported(int dtype, int head_dim, bool paged, int page_size)
 int decode_stream_waves(int stages, int group);  // resident one-wave workgroups on this device
 int decode_stream_qrows(int group);               // query rows per partial slot
 hipError_t launch_decode_stream(const DecodeParams& p, int dtype, bool paged, hipStream_t stream);
+
+// Cache writes (cache_ops.hip). positions: device int32, read at
+// b * pos_stride (pos_stride 0 = one position for the whole batch).
+struct KvWriteParams {
+  const void* k;  // [B, Hkv, L, D] rows to write
+  const void* v;
+  void* k_cache;  // [B, Hkv, C, D]
+  void* v_cache;
+  const int32_t* positions;
+  int pos_stride;
+  int B, Hkv, L, C;
+  int ring;  // 0: slot pos + i; 1: slot (pos + i) % C, last C rows only
+};
+hipError_t launch_kv_cache_write(const KvWriteParams& p, int dtype, int head_dim, hipStream_t stream);
+
+struct PagedWriteParams {
+  const void* k;  // [B, Hkv, L, D]
+  const void* v;
+  void* k_pages;  // [num_pages, Hkv, page_size, D]
+  void* v_pages;
+  const int32_t* block_tables;  // [B, pages_per_seq]
+  const int32_t* positions;
+  int pos_stride;
+  int B, Hkv, L, num_pages, page_size, pages_per_seq;
+};
+hipError_t launch_paged_cache_write(const PagedWriteParams& p, int dtype, int head_dim, hipStream_t stream);
+
+// Fused decode step: prologue (RoPE of q and the new k at the token's
+// position, cache-slot write, per-batch live length) before the streaming
+// decode over the device-side lengths.
+struct DecodeStepParams {
+  const void* q;      // [B, Hq, D] pre-RoPE query of the new token
+  const void* k_new;  // [B, Hkv, D] pre-RoPE key
+  const void* v_new;  // [B, Hkv, D]
+  void* k_cache;      // [B, Hkv, C, D]
+  void* v_cache;
+  void* q_rot;        // [B, Hq, D] workspace: rotated query
+  int32_t* kv_lens;   // [B] workspace: live keys per batch
+  const int32_t* positions;
+  int pos_stride;
+  const float* cos;   // [rope_len, D] or null (no rotation)
+  const float* sin;
+  int rope_len;
+  int B, Hq, Hkv, C;
+  int ring;
+};
+hipError_t launch_decode_step_prep(const DecodeStepParams& p, int dtype, int head_dim, hipStream_t stream);
 
 }  // namespace pf

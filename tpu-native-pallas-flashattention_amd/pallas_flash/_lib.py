@@ -76,6 +76,35 @@ class PagedArgs(ctypes.Structure):
     ]
 
 
+class KvWriteArgs(ctypes.Structure):
+    _fields_ = [
+        ("k", c_ptr), ("v", c_ptr), ("k_cache", c_ptr), ("v_cache", c_ptr),
+        ("positions", c_ptr), ("positions_stride", c_i32),
+        ("batch", c_i32), ("num_kv_heads", c_i32), ("seq_len", c_i32), ("cache_size", c_i32),
+        ("head_dim", c_i32), ("ring", c_i32), ("dtype", c_i32),
+    ]
+
+
+class PagedWriteArgs(ctypes.Structure):
+    _fields_ = [
+        ("k", c_ptr), ("v", c_ptr), ("k_pages", c_ptr), ("v_pages", c_ptr),
+        ("block_tables", c_ptr), ("positions", c_ptr), ("positions_stride", c_i32),
+        ("batch", c_i32), ("num_kv_heads", c_i32), ("seq_len", c_i32), ("num_pages", c_i32),
+        ("page_size", c_i32), ("head_dim", c_i32), ("pages_per_seq", c_i32), ("dtype", c_i32),
+    ]
+
+
+class DecodeStepArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_ptr), ("k_new", c_ptr), ("v_new", c_ptr), ("k_cache", c_ptr), ("v_cache", c_ptr),
+        ("o", c_ptr), ("positions", c_ptr), ("positions_stride", c_i32),
+        ("cos", c_ptr), ("sin", c_ptr), ("rope_len", c_i32),
+        ("batch", c_i32), ("num_heads", c_i32), ("num_kv_heads", c_i32), ("cache_size", c_i32),
+        ("head_dim", c_i32), ("ring", c_i32), ("sm_scale", c_f32), ("dtype", c_i32),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 # (symbol, argtypes, restype) for every entry point the header declares.
 SIGNATURES = {
     "pf_attn_fwd": ([ctypes.POINTER(FwdArgs), c_ptr], ctypes.c_int),
@@ -89,6 +118,10 @@ SIGNATURES = {
     "pf_attn_decode": ([ctypes.POINTER(DecodeArgs), c_ptr], ctypes.c_int),
     "pf_paged_attn_workspace_size": ([ctypes.POINTER(PagedArgs)], ctypes.c_size_t),
     "pf_paged_attn": ([ctypes.POINTER(PagedArgs), c_ptr], ctypes.c_int),
+    "pf_kv_cache_write": ([ctypes.POINTER(KvWriteArgs), c_ptr], ctypes.c_int),
+    "pf_paged_cache_write": ([ctypes.POINTER(PagedWriteArgs), c_ptr], ctypes.c_int),
+    "pf_attn_decode_step_workspace_size": ([ctypes.POINTER(DecodeStepArgs)], ctypes.c_size_t),
+    "pf_attn_decode_step": ([ctypes.POINTER(DecodeStepArgs), c_ptr], ctypes.c_int),
     "pf_version": ([], ctypes.c_char_p),
 }
 

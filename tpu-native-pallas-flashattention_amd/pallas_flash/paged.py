@@ -106,22 +106,54 @@ def init_paged_cache(num_pages: int, num_kv_heads: int, page_size: int, head_dim
             torch.zeros(shape, dtype=dtype, device=device))
 
 
-def write_to_paged_cache(k_pages, v_pages, k, v, block_table, position: int):
-    """Write one token's K/V into the page holding ``position`` (paged.py:205-223).
+def write_to_paged_cache(k_pages, v_pages, k, v, block_table, position):
+    """Write token K/V into the pages holding their positions
+    (paged.py:205-223), on device (pf_paged_cache_write), in place.
 
-    Args:
-        k, v: ``[1, num_kv_heads, 1, head_dim]`` for a single token.
-        block_table: ``[pages_per_seq]`` table of this sequence.
-        position: absolute token position being written.
+    The reference writes one token of one sequence: ``k``/``v``
+    ``[1, num_kv_heads, 1, head_dim]``, ``block_table`` ``[pages_per_seq]``,
+    ``position`` an int. The same call also takes a batch: ``k``/``v``
+    ``[batch, num_kv_heads, seq_len, head_dim]``, ``block_table``
+    ``[batch, pages_per_seq]`` and ``position`` an int or ``[batch]``
+    integers (row ``i`` of sequence ``b`` goes to position
+    ``position[b] + i``). A row whose position falls outside the table, or
+    whose table entry is not a page of the pool (e.g. ``-1`` padding), is not
+    written (the reference's dynamic_update_slice would clamp it onto a valid
+    slot).
 
-    Returns the updated ``(k_pages, v_pages)`` (updated in place and returned,
-    so the reference's functional call pattern keeps working).
+    Returns the updated ``(k_pages, v_pages)`` (the same tensors), so the
+    reference's functional call pattern keeps working.
     """
-    page_size = k_pages.shape[2]
-    logical_page, offset = divmod(int(position), page_size)
-    physical_page = int(torch.as_tensor(block_table)[logical_page])
-    k_pages[physical_page, :, offset] = k[0, :, 0].to(k_pages.dtype)
-    v_pages[physical_page, :, offset] = v[0, :, 0].to(v_pages.dtype)
+    from .cache import _check_positions, _positions
+    if k_pages.dim() != 4 or k_pages.shape != v_pages.shape:
+        raise ValueError("k_pages and v_pages must be [num_pages, num_kv_heads, page_size, head_dim] of one shape")
+    if k.dim() != 4 or k.shape != v.shape:
+        raise ValueError("k and v must be [batch, num_kv_heads, seq_len, head_dim] of one shape")
+    num_pages, hkv, page_size, d = k_pages.shape
+    batch = k.shape[0]
+    if k.shape[1] != hkv or k.shape[3] != d:
+        raise ValueError(f"k {tuple(k.shape)} does not match the pool {tuple(k_pages.shape)}")
+    if k_pages.dtype != v_pages.dtype:
+        raise ValueError("k_pages and v_pages must share a dtype")
+    table = torch.as_tensor(block_table)
+    if table.dim() == 1:
+        table = table.unsqueeze(0)
+    if table.dim() != 2 or table.shape[0] != batch:
+        raise ValueError(f"block_table must be [pages_per_seq] or [batch, pages_per_seq], got {tuple(table.shape)}")
+    _check_positions(position, batch)
+    _lib.require_device(k_pages, v_pages, k, v)
+    if not (k_pages.is_contiguous() and v_pages.is_contiguous()):
+        raise ValueError("the page pools are written in place and must be contiguous")
+    dev = k_pages.device
+    table = table.to(device=dev, dtype=torch.int32).contiguous()
+    pos, stride = _positions(position, batch, dev)
+    k = k.to(k_pages.dtype).contiguous()
+    v = v.to(k_pages.dtype).contiguous()
+    args = _lib.PagedWriteArgs(_lib.ptr(k), _lib.ptr(v), _lib.ptr(k_pages), _lib.ptr(v_pages), _lib.ptr(table),
+                               _lib.ptr(pos), stride, batch, hkv, k.shape[2], num_pages, page_size, d,
+                               table.shape[1], _lib.dtype_tag(k_pages))
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().pf_paged_cache_write(args, _lib.stream_of(k_pages)), "write_to_paged_cache")
     return k_pages, v_pages
 
 
