@@ -98,6 +98,29 @@ size_t pf_attn_fwd_rope_workspace_size(const pf_attn_fwd_rope_args* args);
 int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * RoPE rotation of a [batch, heads, seq_len, head_dim] tensor, the rotation
+ * the fused forward applies (rotate-half, fused_rope.py:43-50; model.py:54-67):
+ *   inverse = 0: out = x*cos + rotate_half(x)*sin
+ *   inverse = 1: out = x*cos - rotate_half(x)*sin   (the transpose rotation:
+ *               the VJP of the forward one -- the RoPE-aware backward; the
+ *               reference's fused kernel is forward-only, README.md:156-157)
+ * Row s of every (batch, head) uses table row s; float32 arithmetic, one
+ * rounding to dtype. x and out may alias.
+ *   cos, sin [rope_len, head_dim] float32 with rope_len >= seq_len
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* x;
+  void* out;
+  const float* cos;
+  const float* sin;
+  int32_t batch, heads, seq_len, head_dim, rope_len;
+  int32_t inverse;
+  int32_t dtype;
+} pf_rope_args;
+
+int pf_rope(const pf_rope_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Backward. Replaces `_flash_attention_bwd_call` (flash_attention.py:354-442):
  * the delta preprocess (:363-365), the `flash_attention_bwd_dq` pallas_call
  * (:379-398) and the `flash_attention_bwd_dkv` pallas_call plus the GQA group

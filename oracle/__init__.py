@@ -21,6 +21,7 @@ from .attention import (  # noqa: F401
     precompute_rope_ref,
     apply_rope_ref,
     rope_attention_ref,
+    rope_attention_bwd_ref,
     decode_ref,
     paged_ref,
     gather_pages_ref,

@@ -35,7 +35,7 @@ def test_header_declares_expected_entry_points():
                  "pf_attn_bwd", "pf_attn_bwd_delta",
                  "pf_attn_bwd_dq", "pf_attn_bwd_dkv", "pf_attn_decode",
                  "pf_attn_decode_workspace_size", "pf_paged_attn", "pf_paged_attn_workspace_size",
-                 "pf_kv_cache_write", "pf_paged_cache_write", "pf_attn_decode_step",
+                 "pf_rope", "pf_kv_cache_write", "pf_paged_cache_write", "pf_attn_decode_step",
                  "pf_attn_decode_step_workspace_size", "pf_version"):
         assert want in names
 
@@ -57,6 +57,7 @@ def test_struct_sizes_match_c_layout():
     assert ctypes.sizeof(_lib.BwdArgs) == 10 * 8 + 10 * 4
     assert ctypes.sizeof(_lib.DecodeArgs) == 4 * 8 + 8 * 4 + 8 + 8
     assert ctypes.sizeof(_lib.PagedArgs) == 6 * 8 + 9 * 4 + 4 + 8 + 8
+    assert ctypes.sizeof(_lib.RopeArgs) == 4 * 8 + 7 * 4 + 4
     assert ctypes.sizeof(_lib.KvWriteArgs) == 5 * 8 + 8 * 4
     assert ctypes.sizeof(_lib.PagedWriteArgs) == 6 * 8 + 9 * 4 + 4
     # 7 pointers, stride + pad, cos/sin, 9 x 4-byte fields + pad, workspace, size_t
@@ -236,3 +237,22 @@ def test_decode_step_workspace_and_rejections(L):
         assert L.pf_attn_decode_step_workspace_size(_step(**over)) == 0, over
     # no tables: no rotation, still valid
     assert L.pf_attn_decode_step_workspace_size(_step(cos=None, sin=None, rope_len=0)) == ws
+
+
+def _rope_args(**over):
+    base = dict(x=8, out=8, cos=8, sin=8, batch=1, heads=2, seq_len=64, head_dim=128, rope_len=64,
+                inverse=0, dtype=1)
+    base.update(over)
+    return _lib.RopeArgs(**base)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(rope_len=63), _lib.PF_ERR_INVALID),        # table shorter than the rows
+    (dict(head_dim=127), _lib.PF_ERR_INVALID),       # odd head_dim (fused_rope.py:168-169)
+    (dict(inverse=2), _lib.PF_ERR_INVALID),
+    (dict(sin=None), _lib.PF_ERR_INVALID),
+    (dict(head_dim=96), _lib.PF_ERR_UNSUPPORTED),
+    (dict(seq_len=0, x=None, out=None), _lib.PF_OK),
+])
+def test_rope_rejects_on_host(L, over, status):
+    assert L.pf_rope(_rope_args(**over), None) == status

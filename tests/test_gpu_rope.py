@@ -1,4 +1,5 @@
-"""GPU tier: fused-RoPE forward kernel vs the oracle and vs the unfused path.
+"""GPU tier: fused-RoPE attention vs the oracle and vs the unfused path, and
+its RoPE-aware backward vs the chain rule over the oracle forward.
 
 Re-expresses the reference's test_fused_rope.py (fused == unfused for
 MHA/GQA/MQA x causal :26-39, ragged :42-50, decode with separate tables at
@@ -97,10 +98,66 @@ def test_precompute_rope_matches_closed_form():
     assert max_abs(host(cos[:64]), rc[:64]) < 1e-5
 
 
-def test_rope_is_forward_only():
-    q, k, v = _inputs(2, 2, 64, seed=5)
-    cos, sin = precompute_rope(64, 128, THETA, device="cuda")
-    tq = dev(q, "f32").requires_grad_(True)
-    out = flash_attention_rope(tq, dev(k, "f32"), dev(v, "f32"), cos, sin)
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
+def _grad_case(dt, Hq, Hkv, S, causal, kv_len, seed):
+    from gpu_util import check_grad
+    from oracle import rope_attention_bwd_ref
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((2, Hq, S, 128))
+    k = rng.standard_normal((2, Hkv, S, 128))
+    v = rng.standard_normal((2, Hkv, S, 128))
+    do = rng.standard_normal((2, Hq, S, 128))
+    cos, sin = precompute_rope(S, 128, THETA, device="cuda")
+    tq, tk, tv = (dev(x, dt).requires_grad_(True) for x in (q, k, v))
+    tdo = dev(do, dt)
+    out = flash_attention_rope(tq, tk, tv, cos, sin, causal=causal, kv_len=kv_len)
+    out.backward(tdo)
+    torch.cuda.synchronize()
+    c, s_ = host(cos), host(sin)
+    ref_o = rope_attention_ref(host(tq), host(tk), host(tv), c, s_, causal=causal, kv_len=kv_len)
+    check_fwd(host(out), ref_o, dt)
+    gq, gk, gv = rope_attention_bwd_ref(host(tq), host(tk), host(tv), host(tdo), c, s_, causal=causal,
+                                        kv_len=kv_len)
+    for name, got, want in (("dq", tq.grad, gq), ("dk", tk.grad, gk), ("dv", tv.grad, gv)):
+        check_grad(host(got), want, dt, name)
+    if kv_len is not None:  # keys past kv_len: exactly zero gradient through the inverse rotation too
+        assert not host(tk.grad)[:, :, kv_len:].any() and not host(tv.grad)[:, :, kv_len:].any()
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("Hq,Hkv,causal", [(4, 2, True), (4, 4, False), (8, 2, True)])
+def test_rope_backward_matches_oracle(dt, Hq, Hkv, causal):
+    """RoPE-aware VJP (the reference's fused kernel is forward-only,
+    README.md:156-157): gradients vs the chain rule over the oracle forward."""
+    note(f"rope backward dt={dt} Hq={Hq} Hkv={Hkv} causal={causal}")
+    _grad_case(dt, Hq, Hkv, 192, causal, None, 21)
+
+
+def test_rope_backward_kv_len():
+    note("rope backward kv_len")
+    _grad_case("bf16", 4, 2, 160, False, 100, 22)
+
+
+def test_rope_training_forward_matches_inference_forward():
+    """The autograd path (rotate once, LSE forward) and the forward-only fused
+    kernel produce the same output."""
+    q, k, v = _inputs(4, 2, 256, seed=23)
+    cos, sin = precompute_rope(256, 128, THETA, device="cuda")
+    tq, tk, tv = dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16")
+    inf = flash_attention_rope(tq, tk, tv, cos, sin, causal=True)
+    train = flash_attention_rope(tq.clone().requires_grad_(True), tk, tv, cos, sin, causal=True)
+    assert max_abs(host(inf), host(train.detach())) <= 2e-2
+
+
+def test_rope_rotation_inverse_round_trip():
+    """pf_rope: the transpose rotation undoes the forward one (float32)."""
+    from pallas_flash.fused_rope import _rope
+    rng = np.random.default_rng(24)
+    x = dev(rng.standard_normal((2, 3, 100, 128)), "f32")
+    cos, sin = precompute_rope(128, 128, THETA, device="cuda")
+    y = _rope(x, cos, sin, False)
+    back = _rope(y, cos, sin, True)
+    torch.cuda.synchronize()
+    assert max_abs(host(back), host(x)) < 1e-5
+    c, s_ = precompute_rope_ref(100, 128, THETA)
+    from oracle import apply_rope_ref
+    assert max_abs(host(y), apply_rope_ref(host(x), c, s_)) < 1e-4

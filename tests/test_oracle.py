@@ -452,3 +452,38 @@ def test_decode_step_rope_relative_position_invariance(rng):
     o_plain, kc_plain, _ = decode_step_ref(q0, kn, vn, kc, vc, 0)
     np.testing.assert_allclose(o_rot, o_plain, rtol=0, atol=1e-12)
     np.testing.assert_allclose(kc_rot, kc_plain, rtol=0, atol=1e-12)
+
+
+# ----------------------------------------------------- RoPE-aware backward --
+from oracle import rope_attention_bwd_ref  # noqa: E402
+
+
+@pytest.mark.parametrize("causal,Hq,Hkv,Sq,Sk,kv_len", [(True, 2, 1, 5, 5, None), (False, 4, 2, 3, 6, 5)])
+def test_rope_backward_matches_finite_differences(rng, causal, Hq, Hkv, Sq, Sk, kv_len):
+    D = 6
+    q, k, v = _qkv(rng, 1, Hq, Hkv, Sq, Sk, D)
+    do = rng.standard_normal(q.shape)
+    qc, qs = precompute_rope_ref(Sq + 3, D, 50.0)
+    kc, ks = precompute_rope_ref(Sk + 3, D, 50.0)
+    qc, qs = qc[3:], qs[3:]          # query positions 3.. (decode-like offset)
+    kc, ks = kc[:Sk], ks[:Sk]
+    kw = dict(causal=causal, kv_len=kv_len, sm_scale=0.6)
+    dq, dk, dv = rope_attention_bwd_ref(q, k, v, do, qc, qs, kc, ks, **kw)
+
+    def loss():
+        return float((rope_attention_ref(q, k, v, qc, qs, kc, ks, **kw) * do).sum())
+
+    eps = 1e-6
+    for x, g in ((q, dq), (k, dk), (v, dv)):
+        num = np.zeros_like(x)
+        it = np.nditer(x, flags=["multi_index"])
+        for _ in it:
+            idx = it.multi_index
+            old = x[idx]
+            x[idx] = old + eps
+            fp = loss()
+            x[idx] = old - eps
+            fm = loss()
+            x[idx] = old
+            num[idx] = (fp - fm) / (2 * eps)
+        np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-7)

@@ -355,6 +355,20 @@ int pf_paged_attn(const pf_paged_attn_args* a, void* stream) {
   return finish(pf::launch_decode(p, a->dtype, true, (hipStream_t)stream));
 }
 
+int pf_rope(const pf_rope_args* a, void* stream) {
+  if (!a) return PF_ERR_INVALID;
+  if (a->batch < 0 || a->heads < 0 || a->seq_len < 0 || a->head_dim < 2 || a->head_dim % 2 != 0)
+    return PF_ERR_INVALID;
+  if (a->inverse != 0 && a->inverse != 1) return PF_ERR_INVALID;
+  if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if ((int64_t)a->batch * a->heads * a->seq_len == 0) return PF_OK;
+  if (!a->x || !a->out || !a->cos || !a->sin || a->rope_len < a->seq_len) return PF_ERR_INVALID;
+  return finish(pf::launch_rope_rotate_k(a->x, a->out, a->cos, a->sin, a->batch, a->heads, a->seq_len,
+                                         a->seq_len, a->dtype, a->head_dim, (hipStream_t)stream,
+                                         a->inverse != 0));
+}
+
 // ---------------------------------------------------------------------------
 // Cache writes and the fused decode step
 // ---------------------------------------------------------------------------

@@ -28,10 +28,12 @@ struct FwdParams {
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream);
 
-// Rotate K rows [0, kv_len) of every (batch, kv head) into k_out (same layout
-// as k): x*cos + rotate_half(x)*sin with the [Sk, D] float32 tables.
+// Rotate rows [0, kv_len) of every (batch, head) of a [B, H, Sk, D] tensor
+// into k_out (same layout): x*cos + rotate_half(x)*sin with the [>= kv_len, D]
+// float32 tables (row = position); inverse: x*cos - rotate_half(x)*sin.
 hipError_t launch_rope_rotate_k(const void* k, void* k_out, const float* cos, const float* sin, int B,
-                                int Hkv, int Sk, int kv_len, int dtype, int head_dim, hipStream_t stream);
+                                int Hkv, int Sk, int kv_len, int dtype, int head_dim, hipStream_t stream,
+                                bool inverse = false);
 
 // Backward.
 struct BwdParams {

@@ -76,6 +76,14 @@ class PagedArgs(ctypes.Structure):
     ]
 
 
+class RopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_ptr), ("out", c_ptr), ("cos", c_ptr), ("sin", c_ptr),
+        ("batch", c_i32), ("heads", c_i32), ("seq_len", c_i32), ("head_dim", c_i32), ("rope_len", c_i32),
+        ("inverse", c_i32), ("dtype", c_i32),
+    ]
+
+
 class KvWriteArgs(ctypes.Structure):
     _fields_ = [
         ("k", c_ptr), ("v", c_ptr), ("k_cache", c_ptr), ("v_cache", c_ptr),
@@ -118,6 +126,7 @@ SIGNATURES = {
     "pf_attn_decode": ([ctypes.POINTER(DecodeArgs), c_ptr], ctypes.c_int),
     "pf_paged_attn_workspace_size": ([ctypes.POINTER(PagedArgs)], ctypes.c_size_t),
     "pf_paged_attn": ([ctypes.POINTER(PagedArgs), c_ptr], ctypes.c_int),
+    "pf_rope": ([ctypes.POINTER(RopeArgs), c_ptr], ctypes.c_int),
     "pf_kv_cache_write": ([ctypes.POINTER(KvWriteArgs), c_ptr], ctypes.c_int),
     "pf_paged_cache_write": ([ctypes.POINTER(PagedWriteArgs), c_ptr], ctypes.c_int),
     "pf_attn_decode_step_workspace_size": ([ctypes.POINTER(DecodeStepArgs)], ctypes.c_size_t),

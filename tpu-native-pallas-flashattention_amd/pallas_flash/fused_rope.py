@@ -5,9 +5,15 @@ Drop-in for the reference's ``pallas_flash.fused_rope.flash_attention_rope``
 ``x * cos + rotate_half(x) * sin``. Q is rotated in registers inside the HIP
 attention kernel; K is rotated exactly once per position by a prologue kernel
 into a workspace the attention kernel streams (the reference re-rotates every
-K tile for every query head and query block). Forward only, like the
-reference (its docstring: "for training use the differentiable
-flash_attention with RoPE applied outside").
+K tile for every query head and query block).
+
+Differentiable (a RoPE-aware VJP; the reference is forward-only and tells
+training users to apply RoPE outside, README.md:156-157): when q, k or v
+requires grad, the forward rotates q and k once (pf_rope), runs the
+LSE-saving forward on the rotated tensors and saves them; the backward runs
+the standard backward (pf_attn_bwd) and maps dq, dk back through the
+transpose rotation x*cos - rotate_half(x)*sin (pf_rope, inverse) -- RoPE is
+an orthogonal map per position, so its VJP is its inverse.
 """
 
 from __future__ import annotations
@@ -24,11 +30,33 @@ def _table(t: torch.Tensor, device) -> torch.Tensor:
     return t.to(device=device, dtype=torch.float32).contiguous()
 
 
+def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, inverse: bool) -> torch.Tensor:
+    """Rows s of x [B, H, S, D] rotated with table row s (pf_rope)."""
+    out = torch.empty_like(x)
+    if x.numel() == 0:
+        return out
+    B, H, S, D = x.shape
+    args = _lib.RopeArgs(_lib.ptr(x), _lib.ptr(out), _lib.ptr(cos), _lib.ptr(sin), B, H, S, D, cos.shape[0],
+                         int(inverse), _lib.dtype_tag(x))
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib().pf_rope(args, _lib.stream_of(x)), "rope")
+    return out
+
+
 class _RopeFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, q_cos, q_sin, k_cos, k_sin, causal, sm_scale, kv_len):
+        from .flash_attention import _fwd
         B, Hq, Sq, D = q.shape
         Hkv, Sk = k.shape[1], k.shape[2]
+        ctx.causal, ctx.sm_scale, ctx.kv_len = causal, sm_scale, kv_len
+        if any(ctx.needs_input_grad[:3]):
+            # Training path: rotate once, keep the rotated q/k, o and LSE.
+            q_rot = _rope(q, q_cos, q_sin, False)
+            k_rot = _rope(k, k_cos, k_sin, False)
+            o, lse = _fwd(q_rot, k_rot, v, causal, sm_scale, kv_len, True)
+            ctx.save_for_backward(q_rot, k_rot, v, o, lse, q_cos, q_sin, k_cos, k_sin)
+            return o
         o = torch.empty_like(q)
         if o.numel() == 0:
             return o
@@ -48,9 +76,12 @@ class _RopeFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do):
-        raise NotImplementedError(
-            "flash_attention_rope is forward-only (as in the reference); for training apply "
-            "RoPE outside and use flash_attention")
+        from .flash_attention import _bwd
+        q_rot, k_rot, v, o, lse, q_cos, q_sin, k_cos, k_sin = ctx.saved_tensors
+        dq_rot, dk_rot, dv = _bwd(q_rot, k_rot, v, o, lse, do, ctx.causal, ctx.sm_scale, ctx.kv_len)
+        dq = _rope(dq_rot, q_cos, q_sin, True)
+        dk = _rope(dk_rot, k_cos, k_sin, True)
+        return dq, dk, dv, None, None, None, None, None, None, None
 
 
 def flash_attention_rope(
