@@ -14,6 +14,9 @@ Secondary figures in the same line (each timed with HIP events):
   rope_tflops   config 2 fused-RoPE prefill, bf16 causal GQA B=4 Hq=32 Hkv=8 S=4096
   decode_gbs    config 4 decode, B=64 Hq=32 Hkv=8, cache 8192 with kv_len 6000
                 (slots past 6000 NaN); algorithmic bytes = valid K/V once + q + o
+  decode_step_gbs  config 4's shape as one fused decode step (RoPE of the new
+                token at position 5999, cache-slot write, attention over 6000
+                slots; position in device memory)
   paged_gbs     config 5 paged decode, 128 seqs, page 64, lens U[512, 8192] from
                 np.random.default_rng(0), 16384-page pool, -1-padded table,
                 unreferenced pages and tails NaN; bytes = valid K/V + q + o +
@@ -184,6 +187,46 @@ def bench_decode(L, _lib, torch, iters):
     return ev.mean_ms(0, 1), nbytes
 
 
+def bench_decode_step(L, _lib, torch, iters):
+    """Config 4's shape as a fused decode step (pf_attn_decode_step): RoPE of
+    the new token's q/k at position 5999, cache-slot write, attention over the
+    6000 live slots (device-side position). Bytes = the config-4 decode bytes
+    + the new k/v rows read and written + the two table rows."""
+    from pallas_flash import precompute_rope
+    B, Hq, Hkv, cap, D, pos = 64, 32, 8, 8192, 128, 5999
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    kn = torch.randn((B, Hkv, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    vn = torch.randn((B, Hkv, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    kc = torch.empty((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    for t in (kc, vc):
+        t[:, :, :pos].copy_(torch.randn((B, Hkv, pos, D), generator=g, device="cuda"))
+        t[:, :, pos:].fill_(float("nan"))
+    cos, sin = precompute_rope(cap, D, 10000.0, device="cuda")
+    positions = torch.full((B,), pos, dtype=torch.int32, device="cuda")
+    o = torch.empty_like(q)
+    args = _lib.DecodeStepArgs(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                               o.data_ptr(), positions.data_ptr(), 1, cos.data_ptr(), sin.data_ptr(), cap,
+                               B, Hq, Hkv, cap, D, 0, 1.0 / D ** 0.5, 1, None, 0)
+    ws = _decode_args_and_ws(L, _lib, torch, args, L.pf_attn_decode_step_workspace_size)
+    st = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        ok(L.pf_attn_decode_step(args, st), "pf_attn_decode_step")
+    ev = Events(2, iters)
+    for i in range(iters):
+        ev.mark(i, 0)
+        ok(L.pf_attn_decode_step(args, st), "pf_attn_decode_step")
+        ev.mark(i, 1)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all(), "decode step output not finite"
+    kv_len = pos + 1
+    nbytes = (B * Hkv * kv_len * D * 2 * 2 + 2 * B * Hq * D * 2 + 2 * 2 * B * Hkv * D * 2
+              + 2 * D * 4)
+    del ws
+    return ev.mean_ms(0, 1), nbytes
+
+
 def bench_paged(L, _lib, torch, iters):
     B, Hq, Hkv, D, page, npages, pps = 128, 32, 8, 128, 64, 16384, 128
     rng = np.random.default_rng(0)
@@ -296,7 +339,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "step", "paged", "copy"], default="all")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -327,6 +370,11 @@ def main():
         ms, nb = bench_decode(L, _lib, torch, iters)
         sec["decode_gbs"] = nb / (ms * 1e-3) / 1e9
         sec["decode_ms"] = ms
+    if args.only in ("all", "step"):
+        log("cfg4-shape decode step ...")
+        ms, nb = bench_decode_step(L, _lib, torch, iters)
+        sec["decode_step_gbs"] = nb / (ms * 1e-3) / 1e9
+        sec["decode_step_ms"] = ms
     if args.only in ("all", "paged"):
         log("cfg5 paged ...")
         ms, nb = bench_paged(L, _lib, torch, iters)
@@ -366,6 +414,8 @@ def main():
     line["secondary"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in sec.items()}
     if "decode_gbs" in sec:
         line["secondary"]["decode_frac_hbm"] = round(sec["decode_gbs"] / PEAK_HBM_GBS, 4)
+    if "decode_step_gbs" in sec:
+        line["secondary"]["decode_step_frac_hbm"] = round(sec["decode_step_gbs"] / PEAK_HBM_GBS, 4)
     if "paged_gbs" in sec:
         line["secondary"]["paged_frac_hbm"] = round(sec["paged_gbs"] / PEAK_HBM_GBS, 4)
     if "fwd_tflops" in sec:
