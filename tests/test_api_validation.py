@@ -145,6 +145,8 @@ def test_decode_step_validation_before_device():
         flash_attention_decode_step(q, kn, vn, kc, vc, [0, 1, 2])               # 3 positions for batch 2
     with pytest.raises(ValueError):
         flash_attention_decode_step(q, kn, vn, kc, vc, torch.tensor([0.5, 1.0]))
+    with pytest.raises(ValueError):                                             # model.py:329-331
+        flash_attention_decode_step(q, kn, vn, kc, vc, 64)
     with pytest.raises(RuntimeError):                                           # valid, but no device path
         flash_attention_decode_step(q, kn, vn, kc, vc, 0)
 

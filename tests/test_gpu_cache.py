@@ -287,3 +287,40 @@ def test_decode_step_config4_shape():
     o_ref, _, _ = decode_step_ref(host(q)[sel], host(kn)[sel], host(vn)[sel], kfull, vfull, 5999,
                                   host(cos), host(sin), store=_rounder("bf16"))
     check_fwd(host(o)[sel], o_ref, "bf16")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(8, 2), (4, 4)])
+def test_decode_loop_matches_full_causal_attention(Hq, Hkv):
+    """test_model.py::test_cached_matches_recompute on the attention path:
+    prefill a prompt (write_kv_cache + causal flash_attention on the rotated
+    q/k), then feed the remaining tokens one at a time through
+    flash_attention_decode_step -- every step's output equals the matching row
+    of causal attention over the whole sequence computed at once."""
+    from pallas_flash import apply_rope, flash_attention
+    note(f"decode loop vs full causal Hq={Hq} Hkv={Hkv}")
+    rng = np.random.default_rng(25)
+    B, D, P, T, C = 2, 128, 37, 70, 96  # prompt 37 tokens, 33 decode steps, cache 96
+    q = dev(rng.standard_normal((B, Hq, T, D)), "bf16")
+    k = dev(rng.standard_normal((B, Hkv, T, D)), "bf16")
+    v = dev(rng.standard_normal((B, Hkv, T, D)), "bf16")
+    cos, sin = precompute_rope(C, D, 10000.0, device=DEV)
+    # recompute: rotate the whole sequence (float32, rounded once), causal attention
+    qr = apply_rope(q.float(), cos[:T], sin[:T]).to(torch.bfloat16)
+    kr = apply_rope(k.float(), cos[:T], sin[:T]).to(torch.bfloat16)
+    full = host(flash_attention(qr, kr, v, causal=True))
+    # cached: prefill writes the rotated prompt keys, then one decode step per token
+    kc = torch.zeros((B, Hkv, C, D), dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    write_kv_cache(kc, vc, kr[:, :, :P], v[:, :, :P], 0)
+    pos = torch.full((B,), P, dtype=torch.int32, device=DEV)
+    worst = 0.0
+    for t in range(P, T):
+        o = flash_attention_decode_step(q[:, :, t:t + 1], k[:, :, t:t + 1], v[:, :, t:t + 1], kc, vc, pos,
+                                        cos, sin)
+        worst = max(worst, max_abs(host(o)[:, :, 0], full[:, :, t]))
+        pos += 1
+    torch.cuda.synchronize()
+    assert worst <= 2e-2, f"cached vs recompute max-abs {worst:.3e}"
+    # the cache now holds exactly the rotated keys and values of all T tokens
+    assert max_abs(host(kc[:, :, :T]), host(kr)) <= 2e-2
+    assert torch.equal(vc[:, :, :T], v)

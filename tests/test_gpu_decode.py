@@ -83,3 +83,21 @@ def test_decode_with_grad_routes_through_flash_attention():
     ref = flash_attention(q.detach(), k.detach(), v.detach(), kv_len=40)
     assert torch.allclose(out, ref, atol=1e-6)
     assert (k.grad[:, :, 40:] == 0).all()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_ring_layout_is_permutation_invariant(dt):
+    """test_streaming.py:82-103: decode over a ring rotated by `shift` slots
+    equals decode over the same keys in order, and both match the oracle."""
+    note(f"decode ring permutation dt={dt}")
+    rng = np.random.default_rng(9)
+    capacity, dim = 8, 128
+    q = rng.standard_normal((1, 2, 1, dim))
+    k = rng.standard_normal((1, 2, capacity, dim))
+    v = rng.standard_normal((1, 2, capacity, dim))
+    in_order = host(flash_attention_decode(dev(q, dt), dev(k, dt), dev(v, dt), capacity, block_k=capacity))
+    for shift in (1, 3, 7):
+        rolled = host(flash_attention_decode(dev(q, dt), dev(np.roll(k, shift, axis=2), dt),
+                                             dev(np.roll(v, shift, axis=2), dt), capacity))
+        assert max_abs(in_order, rolled) < (2e-3 if dt == "f32" else 2e-2)
+    check_fwd(in_order, decode_ref(host(dev(q, dt)), host(dev(k, dt)), host(dev(v, dt)), capacity), dt)

@@ -125,7 +125,9 @@ def flash_attention_decode_step(
         k_cache, v_cache: ``[batch, num_kv_heads, capacity, head_dim]``.
         positions: absolute position of the new token: an int, or ``[batch]``
             integers; pass a device int32 tensor to keep the step capturable.
-            An out-of-range position (``ring=False``: outside
+            With ``ring=False`` a host-side position ``>= capacity`` raises
+            ``ValueError`` (as decode_step, model.py:329-331); in device
+            memory, an out-of-range position (``ring=False``: outside
             ``[0, capacity)``; any: negative, or past the RoPE table) writes
             nothing and yields zeros for that batch.
         cos, sin: ``[rope_len, head_dim]`` tables (``precompute_rope``), or
@@ -156,7 +158,11 @@ def flash_attention_decode_step(
             raise ValueError("q, k_new, v_new and the caches must share a dtype")
     if sm_scale is None:
         sm_scale = 1.0 / (d ** 0.5)
-    _check_positions(positions, batch)
+    pos_t, _ = _check_positions(positions, batch)
+    if not ring and pos_t.device.type == "cpu" and pos_t.numel() and int(pos_t.max()) >= cap:
+        # decode_step's host check (model.py:329-331); positions in device
+        # memory are not read back (that would sync) -- the kernel skips them.
+        raise ValueError(f"position {int(pos_t.max())} exceeds cache capacity {cap}")
     tensors = [q, k_new, v_new, k_cache, v_cache] + ([cos, sin] if cos is not None else [])
     _lib.require_device(*tensors)
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
