@@ -142,19 +142,11 @@ __device__ inline u32x4 f32_to_chunk(const float* in) {
   }
 }
 
-// Raw buffer resource over [base, base + bytes): loads at byte offsets at or
-// past `bytes` return zeros without touching memory (hardware bounds check),
-// which is how rows past kv_len are zero-filled without branches.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-__device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ inline u32x4 bufld16(rsrc_t r, uint32_t byte_off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
-}
-
 // Wave-uniform raw buffer descriptor over [base, base + bytes), for the
-// inline-assembly LDS DMA below (base and bytes must be wave-uniform).
+// inline-assembly LDS DMA below (base and bytes must be wave-uniform). Loads
+// at byte offsets at or past `bytes` return zeros without touching memory
+// (hardware bounds check): that is how rows past kv_len, past a page's valid
+// rows or past Sq are zero-filled without branches.
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 __device__ inline i32x4 make_desc(const void* base, uint32_t bytes) {
   const uint64_t a = (uint64_t)base;

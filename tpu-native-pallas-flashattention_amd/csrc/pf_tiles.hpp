@@ -16,7 +16,7 @@
 // The swizzle makes both read kinds and the staging writes conflict-free:
 // the 16 lanes of a natural read hit 16 distinct chunks, and a transposed read
 // (4 consecutive rows x 4 consecutive chunks) hits 16 distinct chunks.
-// Rows at or past a limit are loaded as zeros by the buffer resource.
+// Rows at or past a limit are loaded as zeros by the buffer descriptor.
 #pragma once
 
 #include "pf_common.hpp"
@@ -45,31 +45,6 @@ struct Tile {
   static constexpr int BYTES = 64 * RB;
   static constexpr int PER_T = 64 * CPR / 256;  // chunks staged per thread (256 threads)
   static constexpr bool TR = (ES == 2);
-};
-
-// Register staging of one tile: coalesced 16-byte buffer loads (a wave reads
-// whole rows), then swizzled LDS stores.
-template <typename T, int D>
-struct TileRegs {
-  using G = Tile<T, D>;
-  u32x4 r[G::PER_T];
-
-  __device__ inline void load(rsrc_t rs, int row0, int tid) {
-#pragma unroll
-    for (int u = 0; u < G::PER_T; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / G::CPR, cc = c % G::CPR;
-      r[u] = bufld16(rs, (uint32_t)((row0 + row) * D + cc * G::EPC) * G::ES);
-    }
-  }
-  __device__ inline void store(char* tile, int tid) const {
-#pragma unroll
-    for (int u = 0; u < G::PER_T; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / G::CPR, cc = c % G::CPR;
-      sts16(tile + row * G::RB + 16 * (cc ^ tile_swz<G::CPR>(row)), r[u]);
-    }
-  }
 };
 
 // Direct global -> LDS staging (dma16): lane l of a wave writes its 16 bytes
