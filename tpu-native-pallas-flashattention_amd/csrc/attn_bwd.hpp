@@ -110,6 +110,8 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)G::RB;
   const i32x4 krs = make_desc(Kb, kv_bytes);
   const i32x4 vrs = make_desc(Vb, kv_bytes);
+  TileDma<T, D> dma;
+  dma.init(tid);
   TrAddr<T, D> kta;
   kta.init(lane);
 
@@ -118,8 +120,8 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   const int nblk = (kv_end + BN - 1) / BN;
 
   if (nblk > 0) {
-    TileDma<T, D>::load(krs, 0, smem, tid);
-    TileDma<T, D>::load(vrs, 0, smem + G::BYTES, tid);
+    dma.load(krs, 0, smem);
+    dma.load(vrs, 0, smem + G::BYTES);
   }
   dma_wait();
   __syncthreads();
@@ -138,8 +140,8 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
     const char* sv = sk + G::BYTES;
     if (j + 1 < nblk) {
       char* nk = smem + ((j + 1) & 1) * (2 * G::BYTES);
-      TileDma<T, D>::load(krs, kv0 + BN, nk, tid);
-      TileDma<T, D>::load(vrs, kv0 + BN, nk + G::BYTES, tid);
+      dma.load(krs, kv0 + BN, nk);
+      dma.load(vrs, kv0 + BN, nk + G::BYTES);
     }
     // keys kv0 + 32hh + 16t + r, query qrow. The two 32-key halves t are
     // processed one after the other to keep S^T/dP^T register use small.
@@ -257,13 +259,15 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
     h = kvh * p.g + member;
     qb0 = q_begin + blk * BMQ;
   };
+  TileDma<T, D> dma;
+  dma.init(tid);
   auto load_step = [&](int st, char* buf) {
     int h, qb0;
     step_coords(st, h, qb0);
     const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
     const uint32_t qbytes = (uint32_t)p.Sq * (uint32_t)G::RB;
-    TileDma<T, D>::load(make_desc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, buf, tid);
-    TileDma<T, D>::load(make_desc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, buf + G::BYTES, tid);
+    dma.load(make_desc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, buf);
+    dma.load(make_desc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, buf + G::BYTES);
     // Raw load only: a use here would make the wave wait (vmcnt(0)) for the
     // tile DMA just issued as well; the log2 scaling happens at the store.
     if (tid < 2 * BMQ) {

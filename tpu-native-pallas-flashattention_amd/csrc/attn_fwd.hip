@@ -141,6 +141,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
   const i32x4 krs = make_desc(Kb, kv_bytes);
   const i32x4 vrs = make_desc(Vb, kv_bytes);
+  TileDma<T, D> dma;
+  dma.init(tid);
   // K and V go global -> LDS by DMA (with fused RoPE, p.k is the K rotated
   // once by pf_rope_rotate_k_kernel).
 
@@ -218,9 +220,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 
   f32x16 s_cur[2];
   if (nblk > 0) {
-    TileDma<T, D>::load(krs, 0, kbuf(0), tid);
-    TileDma<T, D>::load(vrs, 0, vbuf(0), tid);
-    if (nblk > 1) TileDma<T, D>::load(krs, BN, kbuf(1), tid);
+    dma.load(krs, 0, kbuf(0));
+    dma.load(vrs, 0, vbuf(0));
+    if (nblk > 1) dma.load(krs, BN, kbuf(1));
     dma_wait();
     __syncthreads();
     s_cur[0] = (f32x16)(0.f);
@@ -236,10 +238,15 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   int n_plain = min(nblk, p.kv_len / BN);
   if constexpr (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
 
-  auto iter = [&](auto masked, int j) {
+  // par = j & 1 as a compile-time constant: the LDS buffer addresses of an
+  // iteration are then fixed and fold into the read instructions' offsets.
+  auto iter = [&](auto masked, int j, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    char* const kcur = kbuf0 + (1 - P) * G::BYTES;  // K_{j+1}
+    char* const vcur = vbuf0 + P * G::BYTES;        // V_j
     const int kv1 = (j + 1) * BN;
-    if (j + 2 < nblk) TileDma<T, D>::load(krs, kv1 + BN, kbuf(j), tid);
-    TileDma<T, D>::load(vrs, kv1, vbuf(j + 1), tid);
+    if (j + 2 < nblk) dma.load(krs, kv1 + BN, kbuf0 + P * G::BYTES);
+    dma.load(vrs, kv1, vbuf0 + (1 - P) * G::BYTES);
     __builtin_amdgcn_sched_barrier(0);
 
     f32x16 s_nxt[2];
@@ -252,16 +259,18 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       // with the max of S_{j+1} beside it (slot = 32 / NV values).
       constexpr int NV1 = G::CPR, VPS1 = 32 / NV1;
       constexpr int NV2 = 4 * NDT, VPS2 = 32 / NV2;
+      // The row sum adds the rounded P (what the P.V product uses), two
+      // values per v_dot2.
       uint32_t pw[16];
       float rs = 0.f;
-      mfma_nat_il<T, D>(kbuf(j + 1), l32, hh, qf, s_nxt[0], s_nxt[1], [&](int i) {
+      mfma_nat_il<T, D>(kcur, l32, hh, qf, s_nxt[0], s_nxt[1], [&](int i) {
 #pragma unroll
         for (int e = 0; e < VPS1; e += 2) {
           const int v = i * VPS1 + e;  // value v = tile v / 16, register v % 16
           const float x0 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][v & 15], c2, -m_run));
           const float x1 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][(v & 15) + 1], c2, -m_run));
-          rs += x0 + x1;
           pw[v >> 1] = pack2<T>(x0, x1);
+          rs = sum2<T>(pw[v >> 1], rs);
         }
       });
       l_run += rs;
@@ -269,7 +278,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       for (int f = 0; f < 4; ++f)
         pfr[f] = __builtin_bit_cast(Frag, (u32x4){pw[4 * f], pw[4 * f + 1], pw[4 * f + 2], pw[4 * f + 3]});
       const int rel = lim - kv1 - 32 * hh;
-      mfma_trn_il<T, D>(vbuf(j), vta, pfr, acc, [&](int i) {
+      mfma_trn_il<T, D>(vcur, vta, pfr, acc, [&](int i) {
 #pragma unroll
         for (int e = 0; e < VPS2; ++e) {
           const int v = i * VPS2 + e;
@@ -283,9 +292,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       });
       mx = wave_xor32_max(mx) * c2;
     } else {
-      mfma_nat<T, D>(kbuf(j + 1), l32, hh, qf, s_nxt[0], s_nxt[1]);
+      mfma_nat<T, D>(kcur, l32, hh, qf, s_nxt[0], s_nxt[1]);
       block_exp(s_cur, pfr);
-      mfma_trn<T, D>(vbuf(j), lane, vta, pfr, acc);
+      mfma_trn<T, D>(vcur, lane, vta, pfr, acc);
       mx = block_max(s_nxt, kv1);
     }
     update_max(mx);
@@ -295,9 +304,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     dma_wait();
     __syncthreads();
   };
+  // Iterations [0, jend) in pairs (even, odd), so each copy's buffers are fixed.
+  using Even = std::integral_constant<int, 0>;
+  using Odd = std::integral_constant<int, 1>;
   int j = 0;
-  for (; j + 1 < min(n_plain, nblk); ++j) iter(std::false_type{}, j);
-  for (; j + 1 < nblk; ++j) iter(std::true_type{}, j);
+  auto run = [&](auto masked, int jend) __attribute__((always_inline)) {
+    if ((j & 1) && j < jend) iter(masked, j++, Odd{});
+    for (; j + 1 < jend; j += 2) {
+      iter(masked, j, Even{});
+      iter(masked, j + 1, Odd{});
+    }
+    if (j < jend) iter(masked, j++, Even{});
+  };
+  run(std::false_type{}, min(n_plain, nblk) - 1);
+  run(std::true_type{}, nblk - 1);
 
   if (nblk > 0) {
     Frag pfr[PF];

@@ -174,9 +174,14 @@ __device__ inline i32x4 make_desc(const void* base, uint32_t bytes) {
 // travels in M0 (an SALU write of M0 read by an LDS DMA needs 1). s_nop 4
 // gives 5.
 __device__ inline void dma16(const i32x4& desc, uint32_t voff, uint32_t lds_addr) {
+  // readfirstlane pins the (uniform) descriptor to SGPRs at this point, where
+  // register pressure could otherwise leave it in VGPRs.
+  i32x4 sd;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sd[i] = __builtin_amdgcn_readfirstlane(desc[i]);
   asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "{m0}"(lds_addr), "v"(voff), "s"(desc)
+               : "{m0}"(lds_addr), "v"(voff), "s"(sd)
                : "memory");
 }
 
