@@ -292,53 +292,109 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   __syncthreads();
 
   // One step: lane = key kkey; half t register r = query qb0 + 32hh + 16t + r.
-  // Program order S/dP of both halves, then per half: P, dS (VALU) and
-  // dV^T += dO^T P, dK^T += Q^T dS (MFMA), so the VALU of one half has the
-  // MFMAs of the other in flight beside it. Every wave runs every step: one
-  // whose keys are all masked for it (past kv_len, causal rows all above its
-  // keys) adds exact zeros (P = dS = 0).
+  // P = exp2(S c - lse) (masked to 0), dS = P (dP - delta); then
+  // dV^T += dO^T P and dK^T += Q^T dS. Every wave runs every step: one whose
+  // keys are all masked for it (past kv_len, causal rows all above its keys)
+  // adds exact zeros (P = dS = 0).
+  // 16-bit: at one wave per SIMD nothing else hides a stall, so the step is
+  // four fenced MFMA sequences with LDS operands read two MFMAs ahead:
+  //   S/dP half 0 | S/dP half 1 + P/dS VALU of half 0 |
+  //   dV/dK of half 0 + P/dS VALU of half 1 | dV/dK of half 1.
   auto step_body = [&](auto masked, const char* sq, const char* sdo, const float* slse, const float* sdl,
                        int qb0) {
     f32x16 sx[2], dx[2];
+    if constexpr (sizeof(T) == 2) {
+      f32x4 lv[2][4], dl[2][4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      sx[t] = (f32x16)(0.f);
-      dx[t] = (f32x16)(0.f);
-      mfma_nat_pair<T, D>(sq, kf, sdo, vf, t, l32, hh, sx[t], dx[t]);
-    }
-    auto half = [&](auto tc) {
-      constexpr int t = decltype(tc)::value;
-      const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
-      const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
-      // P overwrites S and dS overwrites dP.
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const f32x4 lv = l4[r4], dl = d4[r4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * r4 + e;
-          float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lv[e]));
-          if constexpr (decltype(masked)::value) {
-            const int q = qb0 + 32 * hh + 16 * t + r;
-            const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
-            pv = ok ? pv : 0.f;
-          }
-          dx[t][r] = pv * (dx[t][r] - dl[e]);
-          sx[t][r] = pv;
+        for (int r4 = 0; r4 < 4; ++r4) {
+          lv[t][r4] = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t)[r4];
+          dl[t][r4] = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t)[r4];
         }
+      uint32_t pw[2][8], dw[2][8];
+      // value r of half t: P overwrites S and dS overwrites dP; pairs packed.
+      auto pds = [&](auto tc, int r) {
+        constexpr int t = decltype(tc)::value;
+        float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lv[t][r >> 2][r & 3]));
+        if constexpr (decltype(masked)::value) {
+          const int q = qb0 + 32 * hh + 16 * t + r;
+          const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
+          pv = ok ? pv : 0.f;
+        }
+        const float ds = pv * (dx[t][r] - dl[t][r >> 2][r & 3]);
+        sx[t][r] = pv;
+        dx[t][r] = ds;
+        if (r & 1) {
+          pw[t][r >> 1] = pack2<T>(sx[t][r - 1], pv);
+          dw[t][r >> 1] = pack2<T>(dx[t][r - 1], ds);
+        }
+      };
+      auto frags = [&](const uint32_t* w, Frag* f) {
+        f[0] = __builtin_bit_cast(Frag, (u32x4){w[0], w[1], w[2], w[3]});
+        f[1] = __builtin_bit_cast(Frag, (u32x4){w[4], w[5], w[6], w[7]});
+      };
+      using H0 = std::integral_constant<int, 0>;
+      using H1 = std::integral_constant<int, 1>;
+      constexpr int VPS = 16 / G::CPR;  // values per MFMA slot (each sequence has CPR MFMAs)
+      sx[0] = (f32x16)(0.f);
+      dx[0] = (f32x16)(0.f);
+      mfma_nat_pair_il<T, D>(sq, kf, sdo, vf, 0, l32, hh, sx[0], dx[0], [](int) {});
+      sx[1] = (f32x16)(0.f);
+      dx[1] = (f32x16)(0.f);
+      mfma_nat_pair_il<T, D>(sq, kf, sdo, vf, 1, l32, hh, sx[1], dx[1], [&](int i) {
+#pragma unroll
+        for (int e = 0; e < VPS; ++e) pds(H0{}, i * VPS + e);
+      });
+      Frag pf0[2], df0[2];
+      frags(pw[0], pf0);
+      frags(dw[0], df0);
+      mfma_trn2_il<T, D, 0, 2, kAcc>(sdo, pf0, dv, sq, df0, dk, ta, [&](int i) {
+#pragma unroll
+        for (int e = 0; e < VPS; ++e) pds(H1{}, i * VPS + e);
+      });
+      Frag pf1[2], df1[2];
+      frags(pw[1], pf1);
+      frags(dw[1], df1);
+      mfma_trn2_il<T, D, 2, 4, kAcc>(sdo, pf1, dv, sq, df1, dk, ta, [](int) {});
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        sx[t] = (f32x16)(0.f);
+        dx[t] = (f32x16)(0.f);
+        mfma_nat_pair<T, D>(sq, kf, sdo, vf, t, l32, hh, sx[t], dx[t]);
       }
-      // pack_frags(x, x) puts this half's fragments in both slot ranges;
-      // steps [2t, 2t + 2) read the range of half t.
-      Frag pfr[PF], dsf[PF];
-      pack_frags<T>(sx[t], sx[t], pfr);
-      pack_frags<T>(dx[t], dx[t], dsf);
-      // dK/dV accumulate in AGPRs (16-bit): the VGPRs stay free for the
-      // S/dP work and for LDS reads issued ahead of their MFMAs.
-      mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sdo, lane, ta, pfr, dv);
-      mfma_trn<T, D, 2 * t, 2 * t + 2, kAcc>(sq, lane, ta, dsf, dk);
-    };
-    half(std::integral_constant<int, 0>{});
-    half(std::integral_constant<int, 1>{});
+      auto half = [&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        const f32x4* l4 = reinterpret_cast<const f32x4*>(slse + 32 * hh + 16 * t);
+        const f32x4* d4 = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t);
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 lv = l4[r4], dl = d4[r4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lv[e]));
+            if constexpr (decltype(masked)::value) {
+              const int q = qb0 + 32 * hh + 16 * t + r;
+              const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
+              pv = ok ? pv : 0.f;
+            }
+            dx[t][r] = pv * (dx[t][r] - dl[e]);
+            sx[t][r] = pv;
+          }
+        }
+        // pack_frags(x, x) puts this half's fragments in both slot ranges;
+        // steps [2t, 2t + 2) read the range of half t.
+        Frag pfr[PF], dsf[PF];
+        pack_frags<T>(sx[t], sx[t], pfr);
+        pack_frags<T>(dx[t], dx[t], dsf);
+        mfma_trn<T, D, 2 * t, 2 * t + 2>(sdo, lane, ta, pfr, dv);
+        mfma_trn<T, D, 2 * t, 2 * t + 2>(sq, lane, ta, dsf, dk);
+      };
+      half(std::integral_constant<int, 0>{});
+      half(std::integral_constant<int, 1>{});
+    }
   };
 
   int st = 0;
