@@ -297,8 +297,8 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   // keys are all masked for it (past kv_len, causal rows all above its keys)
   // adds exact zeros (P = dS = 0).
   // 16-bit: at one wave per SIMD nothing else hides a stall, so the step is
-  // four fenced MFMA sequences with LDS operands read two MFMAs ahead:
-  //   S/dP half 0 | S/dP half 1 + P/dS VALU of half 0 |
+  // one fenced MFMA sequence with LDS operands read two MFMAs ahead, in four
+  // phases: S/dP half 0 | S/dP half 1 + P/dS VALU of half 0 |
   //   dV/dK of half 0 + P/dS VALU of half 1 | dV/dK of half 1.
   auto step_body = [&](auto masked, const char* sq, const char* sdo, const float* slse, const float* sdl,
                        int qb0) {
@@ -336,27 +336,80 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       };
       using H0 = std::integral_constant<int, 0>;
       using H1 = std::integral_constant<int, 1>;
-      constexpr int VPS = 16 / G::CPR;  // values per MFMA slot (each sequence has CPR MFMAs)
-      sx[0] = (f32x16)(0.f);
-      dx[0] = (f32x16)(0.f);
-      mfma_nat_pair_il<T, D>(sq, kf, sdo, vf, 0, l32, hh, sx[0], dx[0], [](int) {});
-      sx[1] = (f32x16)(0.f);
-      dx[1] = (f32x16)(0.f);
-      mfma_nat_pair_il<T, D>(sq, kf, sdo, vf, 1, l32, hh, sx[1], dx[1], [&](int i) {
+      // One fenced sequence of 4 phases x NP MFMAs (NP = CPR): S/dP half 0,
+      // S/dP half 1, dV/dK half 0, dV/dK half 1. Operands are read LEAD MFMAs
+      // ahead, across phase boundaries too.
+      constexpr int NP = G::CPR, NC = G::CPR / 2, LEAD = 2;
+      constexpr int VPS = 16 / NP;  // P/dS values per MFMA slot
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      const int rs0 = mfma_src_row(l32, 0), rs1 = mfma_src_row(l32, 1);
+      const int sw0 = tile_swz<G::CPR>(rs0), sw1 = tile_swz<G::CPR>(rs1);
+      Frag opnd[LEAD + 1];  // ring: operand of MFMA i in slot i % (LEAD + 1)
+      Frag pf[2][2], df[2][2];
+      sx[0] = sx[1] = dx[0] = dx[1] = (f32x16)(0.f);
+      auto read = [&](int i) __attribute__((always_inline)) {
+        const int ph = i / NP, k = i % NP;
+        if (ph < 2) {
+          // S/dP: k even = Q chunk k/2 (S chain), k odd = dO chunk k/2 (dP chain)
+          const int r = ph ? rs1 : rs0, sw = ph ? sw1 : sw0;
+          const char* tile = (k & 1) ? sdo : sq;
+          opnd[i % (LEAD + 1)] = __builtin_bit_cast(Frag, lds16(tile + r * G::RB + 16 * ((hh * NC + (k >> 1)) ^ sw)));
+        } else {
+          // dV/dK: k even = dO^T (dV), k odd = Q^T (dK); m = k/2: step 2t + m/NDT, block m%NDT
+          const int t = ph - 2, m = k >> 1, c = 2 * t + m / NDT, dt = m % NDT;
+          const char* tile = (k & 1) ? sq : sdo;
+          v4i16 part[2];
 #pragma unroll
-        for (int e = 0; e < VPS; ++e) pds(H0{}, i * VPS + e);
-      });
-      Frag pf0[2], df0[2];
-      frags(pw[0], pf0);
-      frags(dw[0], df0);
-      mfma_trn2_il<T, D, 0, 2, kAcc>(sdo, pf0, dv, sq, df0, dk, ta, [&](int i) {
+          for (int r = 0; r < 2; ++r)
+            part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4i16*)(tile + ta.off[dt][r] + (8 * c + 4 * r) * G::RB));
+          opnd[i % (LEAD + 1)] =
+              __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      };
+      // Phase PH as its own unrolled loop (compile-time phase: every index
+      // below is a constant); MFMA j's operand was read LEAD MFMAs earlier,
+      // possibly in the previous phase.
+      auto phase = [&](auto phc) __attribute__((always_inline)) {
+        constexpr int ph = decltype(phc)::value;
 #pragma unroll
-        for (int e = 0; e < VPS; ++e) pds(H1{}, i * VPS + e);
-      });
-      Frag pf1[2], df1[2];
-      frags(pw[1], pf1);
-      frags(dw[1], df1);
-      mfma_trn2_il<T, D, 2, 4, kAcc>(sdo, pf1, dv, sq, df1, dk, ta, [](int) {});
+        for (int k = 0; k < NP; ++k) {
+          const int j = ph * NP + k;
+          if (j + LEAD < 4 * NP) read(j + LEAD);
+          const Frag& a = opnd[j % (LEAD + 1)];
+          if constexpr (ph < 2) {
+            if (k & 1) dx[ph] = MF::run(a, vf[k >> 1], dx[ph]);
+            else sx[ph] = MF::run(a, kf[k >> 1], sx[ph]);
+            if constexpr (ph == 1) {
+#pragma unroll
+              for (int e = 0; e < VPS; ++e) pds(H0{}, k * VPS + e);
+            }
+          } else {
+            constexpr int t = ph - 2;
+            const int m = k >> 1, cc = m / NDT, dt = m % NDT;
+            f32x16& acc = (k & 1) ? dk[dt] : dv[dt];
+            const Frag& bf = (k & 1) ? df[t][cc] : pf[t][cc];
+            if constexpr (kAcc) MfmaAgpr<T>::run(acc, a, bf);
+            else acc = MF::run(a, bf, acc);
+            if constexpr (ph == 2) {
+#pragma unroll
+              for (int e = 0; e < VPS; ++e) pds(H1{}, k * VPS + e);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+#pragma unroll
+      for (int i = 0; i < LEAD; ++i) read(i);
+      __builtin_amdgcn_sched_barrier(0);
+      phase(std::integral_constant<int, 0>{});
+      phase(std::integral_constant<int, 1>{});
+      frags(pw[0], pf[0]);
+      frags(dw[0], df[0]);
+      phase(std::integral_constant<int, 2>{});
+      frags(pw[1], pf[1]);
+      frags(dw[1], df[1]);
+      phase(std::integral_constant<int, 3>{});
     } else {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
