@@ -261,6 +261,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   };
   TileDma<T, D> dma;
   dma.init(tid);
+  const int wv_u = __builtin_amdgcn_readfirstlane(wv);  // wave index, known uniform
   auto load_step = [&](int st, char* buf) {
     int h, qb0;
     step_coords(st, h, qb0);
@@ -270,10 +271,10 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
     dma.load(make_desc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, buf + G::BYTES);
     // Raw load only: a use here would make the wave wait (vmcnt(0)) for the
     // tile DMA just issued as well; the log2 scaling happens at the store.
-    if (tid < 2 * BMQ) {
-      const int q = min(qb0 + (tid & (BMQ - 1)), p.Sq - 1);
-      lreg = (tid < BMQ ? p.lse : p.delta)[qoff + q];
-    }
+    // wave 0 stages lse, wave 1 delta (a wave-uniform choice: the pointer
+    // stays in scalar registers)
+    const int q = min(qb0 + (tid & (BMQ - 1)), p.Sq - 1);
+    if (wv_u < 2) lreg = (wv_u == 0 ? p.lse : p.delta)[qoff + q];
   };
   auto store_step = [&](char* buf, int st) {
     if (tid < 2 * BMQ) {

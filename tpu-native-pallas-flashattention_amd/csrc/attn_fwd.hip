@@ -232,6 +232,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     update_max(block_max(s_cur, 0));
   }
 
+  // 16-bit: per-lane max of the latest S block, reduced and applied at the
+  // start of the next iteration (or before the last block's exp).
+  float mx_carry = kNegInf;
+
   // Iteration j masks block j + 1. Blocks [0, n_plain) need no mask for any
   // row of the workgroup (below the causal diagonal, inside kv_len), so the
   // iterations run in two straight-line loops: plain max, then masked max.
@@ -255,22 +259,34 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     Frag pfr[PF];
     float mx = kNegInf;
     if constexpr (sizeof(T) == 2) {
-      // S_{j+1} MFMAs with exp/sum/pack of S_j beside them, then O^T += V_j^T P_j
-      // with the max of S_{j+1} beside it (slot = 32 / NV values).
-      constexpr int NV1 = G::CPR, VPS1 = 32 / NV1;
+      // S_{j+1} MFMAs with the max update and exp/sum/pack of S_j beside
+      // them, then O^T += V_j^T P_j with the per-lane max of S_{j+1} beside it
+      // (slot = 32 / NV2 values).
+      constexpr int NV1 = G::CPR;
       constexpr int NV2 = 4 * NDT, VPS2 = 32 / NV2;
       // The row sum adds the rounded P (what the P.V product uses), two
       // values per v_dot2.
       uint32_t pw[16];
       float rs = 0.f;
+      // Slots 0-1: finish the max of S_j (its per-lane part was taken beside
+      // the previous iteration's P.V MFMAs) and update m; slots 2.. : the 16
+      // exp pairs of S_j. The reduction thus runs beside MFMAs instead of
+      // between the last P.V MFMA and the barrier.
+      float mxr = kNegInf;
       mfma_nat_il<T, D>(kcur, l32, hh, qf, s_nxt[0], s_nxt[1], [&](int i) {
+        if (i == 0) {
+          mxr = wave_xor32_max(mx_carry) * c2;
+        } else if (i == 1) {
+          update_max(mxr);
+        } else {
 #pragma unroll
-        for (int e = 0; e < VPS1; e += 2) {
-          const int v = i * VPS1 + e;  // value v = tile v / 16, register v % 16
-          const float x0 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][v & 15], c2, -m_run));
-          const float x1 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][(v & 15) + 1], c2, -m_run));
-          pw[v >> 1] = pack2<T>(x0, x1);
-          rs = sum2<T>(pw[v >> 1], rs);
+          for (int pr = ((i - 2) * 16) / (NV1 - 2); pr < ((i - 1) * 16) / (NV1 - 2); ++pr) {
+            const int v = 2 * pr;  // value v = tile v / 16, register v % 16
+            const float x0 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][v & 15], c2, -m_run));
+            const float x1 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][(v & 15) + 1], c2, -m_run));
+            pw[pr] = pack2<T>(x0, x1);
+            rs = sum2<T>(pw[pr], rs);
+          }
         }
       });
       l_run += rs;
@@ -290,14 +306,13 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
           mx = fmaxf(mx, x);
         }
       });
-      mx = wave_xor32_max(mx) * c2;
+      mx_carry = mx;
     } else {
       mfma_nat<T, D>(kcur, l32, hh, qf, s_nxt[0], s_nxt[1]);
       block_exp(s_cur, pfr);
       mfma_trn<T, D>(vcur, lane, vta, pfr, acc);
-      mx = block_max(s_nxt, kv1);
+      update_max(block_max(s_nxt, kv1));
     }
-    update_max(mx);
     s_cur[0] = s_nxt[0];
     s_cur[1] = s_nxt[1];
 
@@ -320,6 +335,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   run(std::true_type{}, nblk - 1);
 
   if (nblk > 0) {
+    if constexpr (sizeof(T) == 2) update_max(wave_xor32_max(mx_carry) * c2);
     Frag pfr[PF];
     block_exp(s_cur, pfr);
     mfma_trn<T, D>(vbuf(nblk - 1), lane, vta, pfr, acc);
