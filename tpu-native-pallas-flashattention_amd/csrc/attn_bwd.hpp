@@ -143,8 +143,98 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
       dma.load(krs, kv0 + BN, nk);
       dma.load(vrs, kv0 + BN, nk + G::BYTES);
     }
-    // keys kv0 + 32hh + 16t + r, query qrow. The two 32-key halves t are
-    // processed one after the other to keep S^T/dP^T register use small.
+    // keys kv0 + 32hh + 16t + r, query qrow.
+    if constexpr (sizeof(T) == 2) {
+      // One fenced sequence of four phases: S/dP half 0 (NS MFMAs) | S/dP
+      // half 1 + P/dS VALU of half 0 | dQ half 0 (NQ MFMAs) + P/dS VALU of
+      // half 1 | dQ half 1. LDS operands are read LEAD MFMAs ahead, across
+      // the phase boundaries (global MFMA index g; phase starts 0, NS, 2NS,
+      // 2NS + NQ).
+      constexpr int NC = G::CPR / 2, NS = G::CPR, NQ = 2 * NDT, LEAD = 2, RING = 4;
+      constexpr int NTOT = 2 * NS + 2 * NQ;
+      typedef short v4i16 __attribute__((ext_vector_type(4)));
+      const int rs0 = mfma_src_row(l32, 0), rs1 = mfma_src_row(l32, 1);
+      const int sw0 = tile_swz<G::CPR>(rs0), sw1 = tile_swz<G::CPR>(rs1);
+      f32x16 sx[2], dx[2];
+      uint32_t dw[2][8];
+      Frag opnd[RING];
+      Frag dsf[2];
+      sx[0] = sx[1] = dx[0] = dx[1] = (f32x16)(0.f);
+      // value r of half t: dS = P (dP - delta), pairs packed
+      auto pds = [&](auto tc, int r) __attribute__((always_inline)) {
+        constexpr int t = decltype(tc)::value;
+        float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lse2));
+        if constexpr (decltype(masked)::value) {
+          const int key = kv0 + 32 * hh + 16 * t + r;
+          const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
+          pv = ok ? pv : 0.f;
+        }
+        sx[t][r] = pv * (dx[t][r] - dlt);
+        if (r & 1) dw[t][r >> 1] = pack2<T>(sx[t][r - 1], sx[t][r]);
+      };
+      auto read = [&](int g) __attribute__((always_inline)) {
+        if (g < 2 * NS) {
+          // S/dP: k even = K chunk k/2 (S chain), k odd = V chunk k/2 (dP chain)
+          const int t = g / NS, k = g % NS;
+          const int r = t ? rs1 : rs0, sw = t ? sw1 : sw0;
+          const char* tile = (k & 1) ? sv : sk;
+          opnd[g % RING] = __builtin_bit_cast(Frag, lds16(tile + r * G::RB + 16 * ((hh * NC + (k >> 1)) ^ sw)));
+        } else {
+          // dQ: K^T step c = 2t + k / NDT, column block k % NDT
+          const int t = (g - 2 * NS) / NQ, k = (g - 2 * NS) % NQ, c = 2 * t + k / NDT, dt = k % NDT;
+          v4i16 part[2];
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+            part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4i16*)(sk + kta.off[dt][r] + (8 * c + 4 * r) * G::RB));
+          opnd[g % RING] = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      };
+      // phase PH (compile-time): MFMAs g in [g0, g0 + n); P/dS of half vt
+      // (-1: none), its 16 values spread over slots [SK, n).
+      auto phase = [&](auto phc, auto vtc) __attribute__((always_inline)) {
+        constexpr int ph = decltype(phc)::value, vt = decltype(vtc)::value;
+        constexpr int g0 = ph < 2 ? ph * NS : 2 * NS + (ph - 2) * NQ, n = ph < 2 ? NS : NQ;
+        constexpr int SK = ph == 2 ? 2 : 0;  // half 1's S/dP chain ends just before phase 2
+        if constexpr (ph >= 2) {
+          constexpr int t = ph - 2;
+          dsf[0] = __builtin_bit_cast(Frag, (u32x4){dw[t][0], dw[t][1], dw[t][2], dw[t][3]});
+          dsf[1] = __builtin_bit_cast(Frag, (u32x4){dw[t][4], dw[t][5], dw[t][6], dw[t][7]});
+        }
+#pragma unroll
+        for (int k = 0; k < n; ++k) {
+          const int g = g0 + k;
+          if (g + LEAD < NTOT) read(g + LEAD);
+          const Frag& a = opnd[g % RING];
+          if constexpr (ph < 2) {
+            if (k & 1) dx[ph] = MF::run(a, dof[k >> 1], dx[ph]);
+            else sx[ph] = MF::run(a, qf[k >> 1], sx[ph]);
+          } else {
+            acc[k % NDT] = MF::run(a, dsf[k / NDT], acc[k % NDT]);
+          }
+          if constexpr (vt >= 0) {
+            if (k >= SK) {
+#pragma unroll
+              for (int r = ((k - SK) * 16) / (n - SK); r < ((k + 1 - SK) * 16) / (n - SK); ++r)
+                pds(std::integral_constant<int, vt>{}, r);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+#pragma unroll
+      for (int g = 0; g < LEAD; ++g) read(g);
+      __builtin_amdgcn_sched_barrier(0);
+      phase(std::integral_constant<int, 0>{}, std::integral_constant<int, -1>{});
+      phase(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+      phase(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
+      phase(std::integral_constant<int, 3>{}, std::integral_constant<int, -1>{});
+      dma_wait();
+      __syncthreads();
+      return;
+    }
+    // The two 32-key halves t are processed one after the other to keep
+    // S^T/dP^T register use small.
     auto half = [&](auto tc) {
       constexpr int t = decltype(tc)::value;
       f32x16 sx = (f32x16)(0.f), dx = (f32x16)(0.f);
