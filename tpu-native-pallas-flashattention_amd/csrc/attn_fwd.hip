@@ -249,9 +249,28 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     char* const kcur = kbuf0 + (1 - P) * G::BYTES;  // K_{j+1}
     char* const vcur = vbuf0 + P * G::BYTES;        // V_j
     const int kv1 = (j + 1) * BN;
-    if (j + 2 < nblk) dma.load(krs, kv1 + BN, kbuf0 + P * G::BYTES);
-    dma.load(vrs, kv1, vbuf0 + (1 - P) * G::BYTES);
-    __builtin_amdgcn_sched_barrier(0);
+    // DMA of K_{j+2} (into K_j's buffer) and V_{j+1} (into V_{j-1}'s buffer);
+    // both were last read before the barrier that ended iteration j-1.
+    // 16-bit: one load per MFMA slot of the S sequence below, not a burst:
+    // a wave blocked on a full vector-memory queue issues no MFMAs either.
+    char* const kdst = kbuf0 + P * G::BYTES;
+    char* const vdst = vbuf0 + (1 - P) * G::BYTES;
+    const bool k_next = j + 2 < nblk;
+    const i32x4 kd = TileDma<T, D>::at_row(krs, kv1 + BN);
+    const i32x4 vd = TileDma<T, D>::at_row(vrs, kv1);
+    auto dma_part = [&](int i) __attribute__((always_inline)) {
+      constexpr int PT = TileDma<T, D>::PER_T;
+      if (i < PT) {
+        if (k_next) dma.load_part(kd, i, kdst);
+      } else if (i < 2 * PT) {
+        dma.load_part(vd, i - PT, vdst);
+      }
+    };
+    if constexpr (sizeof(T) != 2) {
+      if (k_next) dma.load(krs, kv1 + BN, kdst);
+      dma.load(vrs, kv1, vdst);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
     f32x16 s_nxt[2];
     s_nxt[0] = (f32x16)(0.f);
@@ -264,8 +283,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       // (slot = 32 / NV2 values).
       constexpr int NV1 = G::CPR;
       constexpr int NV2 = 4 * NDT, VPS2 = 32 / NV2;
-      // The row sum adds the rounded P (what the P.V product uses), two
-      // values per v_dot2.
+      // The row sum adds the float32 P (flash_attention.py:127-131: l from
+      // the unrounded p; only the P.V operand is rounded).
       uint32_t pw[16];
       float rs = 0.f;
       // Slots 0-1: finish the max of S_j (its per-lane part was taken beside
@@ -274,6 +293,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       // between the last P.V MFMA and the barrier.
       float mxr = kNegInf;
       mfma_nat_il<T, D>(kcur, l32, hh, qf, s_nxt[0], s_nxt[1], [&](int i) {
+        dma_part(i);
         if (i == 0) {
           mxr = wave_xor32_max(mx_carry) * c2;
         } else if (i == 1) {
@@ -285,7 +305,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
             const float x0 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][v & 15], c2, -m_run));
             const float x1 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][(v & 15) + 1], c2, -m_run));
             pw[pr] = pack2<T>(x0, x1);
-            rs = sum2<T>(pw[pr], rs);
+            rs += x0 + x1;
+            // keeps the sum here: consumed only after the sequence, it would
+            // otherwise sink to the end and hold every exp result live
+            asm volatile("" : "+v"(rs));
           }
         }
       });
@@ -305,6 +328,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
           }
           mx = fmaxf(mx, x);
         }
+        asm volatile("" : "+v"(mx));  // keeps the max beside its MFMA (see rs)
       });
       mx_carry = mx;
     } else {

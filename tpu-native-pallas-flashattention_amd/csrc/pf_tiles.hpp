@@ -45,7 +45,6 @@ struct Tile {
   static constexpr int CPR = D / EPC;      // chunks per row
   static constexpr int RB = D * ES;        // row bytes
   static constexpr int BYTES = 64 * RB;
-  static constexpr int PER_T = 64 * CPR / 256;  // chunks staged per thread (256 threads)
   static constexpr bool TR = (ES == 2);
 };
 
@@ -54,36 +53,50 @@ struct Tile {
 // that belongs at its slot of the swizzled tile. No registers hold the data
 // and no LDS store instructions are issued; the issuing wave must wait for
 // its loads (dma_wait) before the barrier that publishes the tile.
-template <typename T, int D>
+// NW = waves of the workgroup that share the staging (each lane issues
+// PER_T = 64 * CPR / (64 * NW) loads per tile).
+template <typename T, int D, int NW = 4>
 struct TileDma {
   using G = Tile<T, D>;
-  uint32_t voff[G::PER_T];  // this lane's byte offset within the 64 rows
-  uint32_t slot[G::PER_T];  // this wave's LDS byte offset within the tile (uniform)
+  static constexpr int PER_T = G::CPR / NW;
+  static_assert(PER_T >= 1 && G::CPR % NW == 0, "whole 16-byte slots per lane");
+  uint32_t voff[PER_T];  // this lane's byte offset within the 64 rows
+  uint32_t slot[PER_T];  // this wave's LDS byte offset within the tile (uniform)
   // Once per kernel: the lane offsets do not depend on the rows loaded.
   __device__ inline void init(int tid) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
 #pragma unroll
-    for (int u = 0; u < G::PER_T; ++u) {
-      const int s = 64 * (4 * u + w) + l;  // 16-byte slot within the tile
+    for (int u = 0; u < PER_T; ++u) {
+      const int s = 64 * (NW * u + w) + l;  // 16-byte slot within the tile
       const int row = s / G::CPR, phys = s % G::CPR;
       const int chunk = phys ^ tile_swz<G::CPR>(row);
       voff[u] = (uint32_t)(row * D + chunk * G::EPC) * G::ES;
-      slot[u] = 16 * 64 * (4 * u + w);
+      slot[u] = 16 * 64 * (NW * u + w);
     }
   }
-  // Rows [row0, row0 + 64) of the buffer `desc` describes. The descriptor is
-  // moved to row0 (base forward, size shrunk and clamped at 0, so rows past
-  // the end still load as zeros) with scalar arithmetic.
-  __device__ inline void load(const i32x4& desc, int row0, char* tile) const {
+  // The descriptor of rows [row0, ...) of the buffer `desc` describes: base
+  // moved forward and size shrunk (clamped at 0, so rows past the end still
+  // load as zeros), with scalar arithmetic.
+  __device__ static inline i32x4 at_row(const i32x4& desc, int row0) {
     const uint32_t off = (uint32_t)row0 * G::RB;
     const uint64_t base = (((uint64_t)(uint32_t)desc[1] << 32) | (uint32_t)desc[0]) + off;
     i32x4 d = desc;
     d[0] = (int)(uint32_t)base;
     d[1] = (int)(uint32_t)(base >> 32);
     d[2] = (uint32_t)desc[2] > off ? (int)((uint32_t)desc[2] - off) : 0;
-    const uint32_t lds = lds_u32(tile);
+    return d;
+  }
+  // Part u (of PER_T) of a tile load from a descriptor made by at_row: callers
+  // that spread a tile's loads over a compute sequence issue the parts one
+  // at a time.
+  __device__ inline void load_part(const i32x4& d, int u, char* tile) const {
+    dma16(d, voff[u], __builtin_amdgcn_readfirstlane(lds_u32(tile) + slot[u]));
+  }
+  // Rows [row0, row0 + 64) of the buffer `desc` describes.
+  __device__ inline void load(const i32x4& desc, int row0, char* tile) const {
+    const i32x4 d = at_row(desc, row0);
 #pragma unroll
-    for (int u = 0; u < G::PER_T; ++u) dma16(d, voff[u], __builtin_amdgcn_readfirstlane(lds + slot[u]));
+    for (int u = 0; u < PER_T; ++u) load_part(d, u, tile);
   }
 };
 
@@ -402,19 +415,6 @@ __device__ inline uint32_t pack2(float a, float b) {
   typedef T v2 __attribute__((ext_vector_type(2)));
   const v2 x = {Elem<T>::from_f32(a), Elem<T>::from_f32(b)};
   return __builtin_bit_cast(uint32_t, x);
-}
-
-// acc + the sum of the two 16-bit values packed in x: one v_dot2 with (1, 1)
-// (exact products, float32 accumulation).
-template <typename T>
-__device__ inline float sum2(uint32_t x, float acc) {
-  typedef T v2 __attribute__((ext_vector_type(2)));
-  const v2 one = {Elem<T>::from_f32(1.f), Elem<T>::from_f32(1.f)};
-  if constexpr (std::is_same_v<T, bf16_t>) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, x), one, acc, false);
-  } else {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, x), one, acc, false);
-  }
 }
 
 // Pack the 32 values a lane holds (tile t register r <-> reduction slot
