@@ -93,6 +93,26 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const T* Kb = static_cast<const T*>(p.k) + (int64_t)(b * p.Hkv + kvh) * p.Sk * D;
   const T* Vb = static_cast<const T*>(p.v) + (int64_t)(b * p.Hkv + kvh) * p.Sk * D;
 
+  // ---- staging: K/V rows at or past kv_len lie outside the buffer resources
+  // and load as zeros (never read from memory). K and V go global -> LDS by
+  // DMA (with fused RoPE, p.k is the K rotated once by pf_rope_rotate_k_kernel).
+  // The first tiles are requested before Q is loaded (and, with RoPE,
+  // rotated), so the two memory latencies overlap.
+  const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
+  const i32x4 krs = make_desc(Kb, kv_bytes);
+  const i32x4 vrs = make_desc(Vb, kv_bytes);
+  TileDma<T, D> dma;
+  dma.init(tid);
+  int kv_end = p.kv_len;
+  if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + p.rpw, p.Sq));
+  const int nblk = (kv_end + BN - 1) / BN;
+  // LDS: K tiles at [0, 2 BYTES) (block j in j & 1), V tiles after them.
+  if (nblk > 0) {
+    dma.load(krs, 0, smem);
+    dma.load(vrs, 0, smem + 2 * G::BYTES);
+    if (nblk > 1) dma.load(krs, BN, smem + G::BYTES);
+  }
+
   // ---- Q fragment (B operand of S^T): lane holds Q[qrow][hh*HALF, +HALF).
   Frag qf[QF];
   {
@@ -136,15 +156,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
       for (int f = 0; f < FPC; ++f) qf[c * FPC + f] = chunk_frag<T>(qc[c], f);
   }
 
-  // ---- staging: K/V rows at or past kv_len lie outside the buffer resources
-  // and load as zeros (never read from memory).
-  const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
-  const i32x4 krs = make_desc(Kb, kv_bytes);
-  const i32x4 vrs = make_desc(Vb, kv_bytes);
-  TileDma<T, D> dma;
-  dma.init(tid);
-  // K and V go global -> LDS by DMA (with fused RoPE, p.k is the K rotated
-  // once by pf_rope_rotate_k_kernel).
 
   float m_run = kNegInf;  // running max, log2 domain (identical in both halves)
   float l_run = 0.f;      // running sum over this lane half's keys
@@ -152,9 +163,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 #pragma unroll
   for (int i = 0; i < NDT; ++i) acc[i] = (f32x16)(0.f);
 
-  int kv_end = p.kv_len;
-  if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + p.rpw, p.Sq));
-  const int nblk = (kv_end + BN - 1) / BN;
   // c2 = |scale| * log2(e), kept strictly positive so a masked score (-inf)
   // always gives exp2(-inf * c2 - m) = 0 (sm_scale = 0 then yields the mean of
   // the valid V rows up to a ~1e-30 relative perturbation of the weights).
@@ -220,9 +228,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 
   f32x16 s_cur[2];
   if (nblk > 0) {
-    dma.load(krs, 0, kbuf(0));
-    dma.load(vrs, 0, vbuf(0));
-    if (nblk > 1) dma.load(krs, BN, kbuf(1));
     dma_wait();
     __syncthreads();
     s_cur[0] = (f32x16)(0.f);
