@@ -330,31 +330,46 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   TrAddr<T, D> ta;
   ta.init(lane);
 
-  auto step_coords = [&](int st, int& h, int& qb0) {
-    int member, blk;
+  // Step st -> (query head h, query block start qb0), tracked incrementally
+  // (no integer division in the loop): position (a, c) is (member, masked
+  // block index k) while st < n_masked, then (member, descending block index).
+  struct Pos {
+    int a, c;
+  };
+  auto coords = [&](int st, Pos ps, int& h, int& qb0) {
+    int blk;
     if (st < n_masked) {
-      member = st / m_pm;
-      const int k = st - member * m_pm;
-      blk = (all_masked || k < nd) ? k : nqb - 1;
+      blk = (all_masked || ps.c < nd) ? ps.c : nqb - 1;
     } else {
       // Unmasked steps: query blocks from the last one down (outer), group
       // members inner. Workgroups of one (b, kv head) share an XCD and all
       // start at the top block, so at any time they stream the same Q/dO
       // tiles and read them mostly from that XCD's L2.
-      const int jj = st - n_masked;
-      const int desc = jj / p.g;
-      member = jj - desc * p.g;
-      blk = nd + (u_pm - 1 - desc);
+      blk = nd + (u_pm - 1 - ps.c);
     }
-    h = kvh * p.g + member;
+    h = kvh * p.g + ps.a;
     qb0 = q_begin + blk * BMQ;
+  };
+  // position of step st + 1 from that of step st
+  auto advance = [&](int st, Pos ps) -> Pos {
+    if (st + 1 < n_masked) {
+      if (++ps.c == m_pm) {
+        ps.c = 0;
+        ++ps.a;
+      }
+      return ps;
+    }
+    if (st + 1 == n_masked) return Pos{0, 0};
+    if (++ps.a == p.g) {
+      ps.a = 0;
+      ++ps.c;
+    }
+    return ps;
   };
   TileDma<T, D> dma;
   dma.init(tid);
   const int wv_u = __builtin_amdgcn_readfirstlane(wv);  // wave index, known uniform
-  auto load_step = [&](int st, char* buf) {
-    int h, qb0;
-    step_coords(st, h, qb0);
+  auto load_step = [&](int h, int qb0, char* buf) {
     const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
     const uint32_t qbytes = (uint32_t)p.Sq * (uint32_t)G::RB;
     dma.load(make_desc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, buf);
@@ -366,18 +381,19 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
     const int q = min(qb0 + (tid & (BMQ - 1)), p.Sq - 1);
     if (wv_u < 2) lreg = (wv_u == 0 ? p.lse : p.delta)[qoff + q];
   };
-  auto store_step = [&](char* buf, int st) {
+  auto store_step = [&](char* buf, int qb0) {
     if (tid < 2 * BMQ) {
-      int h_unused, qb0;
-      step_coords(st, h_unused, qb0);
       const bool valid = qb0 + (tid & (BMQ - 1)) < p.Sq;
       reinterpret_cast<float*>(buf + 2 * G::BYTES)[tid] = valid ? (tid < BMQ ? lreg * kLog2e : lreg) : 0.f;
     }
   };
 
+  Pos pos{0, 0};  // of step 0 (a masked or an unmasked step alike)
   if (nsteps > 0) {
-    load_step(0, smem);
-    store_step(smem, 0);
+    int h0, qb00;
+    coords(0, pos, h0, qb00);
+    load_step(h0, qb00, smem);
+    store_step(smem, qb00);
   }
   dma_wait();
   __syncthreads();
@@ -547,12 +563,16 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       const char* buf = smem + (st & 1) * BUF;
       const float* slse = reinterpret_cast<const float*>(buf + 2 * G::BYTES);
       int h_unused, qb0;
-      step_coords(st, h_unused, qb0);
+      coords(st, pos, h_unused, qb0);
+      const Pos npos = advance(st, pos);
+      int nh = 0, nqb0 = 0;
       const bool has_next = st + 1 < nsteps;
+      if (has_next) coords(st + 1, npos, nh, nqb0);
       char* const nbuf = smem + ((st + 1) & 1) * BUF;
-      if (has_next) load_step(st + 1, nbuf);
+      if (has_next) load_step(nh, nqb0, nbuf);
       step_body(masked, buf, buf + G::BYTES, slse, slse + BMQ, qb0);
-      if (has_next) store_step(nbuf, st + 1);
+      if (has_next) store_step(nbuf, nqb0);
+      pos = npos;
       dma_wait();
       __syncthreads();
     }
