@@ -159,7 +159,10 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
       uint32_t dw[2][8];
       Frag opnd[RING];
       Frag dsf[2];
-      sx[0] = sx[1] = dx[0] = dx[1] = (f32x16)(0.f);
+      // The dP chains start at -delta (this lane's query), so they end as
+      // dP - delta and dS = P (dP - delta) needs no subtraction.
+      sx[0] = sx[1] = (f32x16)(0.f);
+      dx[0] = dx[1] = (f32x16)(-dlt);
       // value r of half t: dS = P (dP - delta), pairs packed
       auto pds = [&](auto tc, int r) __attribute__((always_inline)) {
         constexpr int t = decltype(tc)::value;
@@ -169,7 +172,7 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
           const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
           pv = ok ? pv : 0.f;
         }
-        sx[t][r] = pv * (dx[t][r] - dlt);
+        sx[t][r] = pv * dx[t][r];
         if (r & 1) dw[t][r >> 1] = pack2<T>(sx[t][r - 1], sx[t][r]);
       };
       auto read = [&](int g) __attribute__((always_inline)) {
@@ -190,17 +193,16 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
           opnd[g % RING] = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
         }
       };
-      // phase PH (compile-time): MFMAs g in [g0, g0 + n); P/dS of half vt
-      // (-1: none), its 16 values spread over slots [SK, n).
-      auto phase = [&](auto phc, auto vtc) __attribute__((always_inline)) {
+      // phase PH (compile-time): MFMAs g in [g0, g0 + n) with P/dS values
+      // [v0, v0 + nv) of half vt (-1: none) spread over slots [SK, NS) of
+      // the phase. dQ phases build each dS fragment right before its first
+      // MFMA, so half 1's second fragment (values 8..15) can be computed
+      // beside the first MFMAs of its own dQ phase.
+      auto phase = [&](auto phc, auto vtc, auto v0c, auto nvc, auto skc, auto sec) __attribute__((always_inline)) {
         constexpr int ph = decltype(phc)::value, vt = decltype(vtc)::value;
+        constexpr int v0 = decltype(v0c)::value, nv = decltype(nvc)::value;
+        constexpr int SK = decltype(skc)::value, SE = decltype(sec)::value;
         constexpr int g0 = ph < 2 ? ph * NS : 2 * NS + (ph - 2) * NQ, n = ph < 2 ? NS : NQ;
-        constexpr int SK = ph == 2 ? 2 : 0;  // half 1's S/dP chain ends just before phase 2
-        if constexpr (ph >= 2) {
-          constexpr int t = ph - 2;
-          dsf[0] = __builtin_bit_cast(Frag, (u32x4){dw[t][0], dw[t][1], dw[t][2], dw[t][3]});
-          dsf[1] = __builtin_bit_cast(Frag, (u32x4){dw[t][4], dw[t][5], dw[t][6], dw[t][7]});
-        }
 #pragma unroll
         for (int k = 0; k < n; ++k) {
           const int g = g0 + k;
@@ -210,13 +212,18 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
             if (k & 1) dx[ph] = MF::run(a, dof[k >> 1], dx[ph]);
             else sx[ph] = MF::run(a, qf[k >> 1], sx[ph]);
           } else {
+            constexpr int t = ph - 2;
+            if (k % NDT == 0) {
+              const int f = k / NDT;
+              dsf[f] = __builtin_bit_cast(Frag, (u32x4){dw[t][4 * f], dw[t][4 * f + 1], dw[t][4 * f + 2], dw[t][4 * f + 3]});
+            }
             acc[k % NDT] = MF::run(a, dsf[k / NDT], acc[k % NDT]);
           }
           if constexpr (vt >= 0) {
-            if (k >= SK) {
+            if (k >= SK && k < SE) {
 #pragma unroll
-              for (int r = ((k - SK) * 16) / (n - SK); r < ((k + 1 - SK) * 16) / (n - SK); ++r)
-                pds(std::integral_constant<int, vt>{}, r);
+              for (int r = ((k - SK) * nv) / (SE - SK); r < ((k + 1 - SK) * nv) / (SE - SK); ++r)
+                pds(std::integral_constant<int, vt>{}, v0 + r);
             }
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -225,10 +232,17 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
 #pragma unroll
       for (int g = 0; g < LEAD; ++g) read(g);
       __builtin_amdgcn_sched_barrier(0);
-      phase(std::integral_constant<int, 0>{}, std::integral_constant<int, -1>{});
-      phase(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
-      phase(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
-      phase(std::integral_constant<int, 3>{}, std::integral_constant<int, -1>{});
+      using I = std::integral_constant<int, 0>;
+      using IM = std::integral_constant<int, -1>;
+      // half 1's S/dP chain ends just before phase 2: its P/dS starts two
+      // slots in; values 8..15 must be done before slot NDT of phase 3
+      phase(I{}, IM{}, I{}, I{}, I{}, I{});
+      phase(std::integral_constant<int, 1>{}, I{}, I{}, std::integral_constant<int, 16>{}, I{},
+            std::integral_constant<int, NS>{});
+      phase(std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{}, I{}, std::integral_constant<int, 8>{},
+            std::integral_constant<int, 2>{}, std::integral_constant<int, NQ>{});
+      phase(std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 8>{},
+            std::integral_constant<int, 8>{}, I{}, std::integral_constant<int, NDT>{});
       dma_wait();
       __syncthreads();
       return;
@@ -429,7 +443,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
           pv = ok ? pv : 0.f;
         }
-        const float ds = pv * (dx[t][r] - dl[t][r >> 2][r & 3]);
+        const float ds = pv * dx[t][r];
         sx[t][r] = pv;
         dx[t][r] = ds;
         if (r & 1) {
@@ -453,7 +467,13 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       const int sw0 = tile_swz<G::CPR>(rs0), sw1 = tile_swz<G::CPR>(rs1);
       Frag opnd[LEAD + 1];  // ring: operand of MFMA i in slot i % (LEAD + 1)
       Frag pf[2][2], df[2][2];
-      sx[0] = sx[1] = dx[0] = dx[1] = (f32x16)(0.f);
+      // The dP chains start at -delta (per query = per register), so they end
+      // as dP - delta and dS = P (dP - delta) needs no subtraction.
+      sx[0] = sx[1] = (f32x16)(0.f);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dx[t][r] = -dl[t][r >> 2][r & 3];
       auto read = [&](int i) __attribute__((always_inline)) {
         const int ph = i / NP, k = i % NP;
         if (ph < 2) {
