@@ -288,14 +288,17 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
   using G = Tile<T, D>;
-  constexpr int BNK = 128, BMQ = 64;
+  // A step covers BMQ query rows of one head as NSUB sub-steps of 64 rows;
+  // 16-bit: 128 rows, so the per-step work (tile DMA issue, lse/delta
+  // staging, DMA wait, barrier) is shared by two sub-steps.
+  constexpr int BNK = 128, BMQ = sizeof(T) == 2 ? 128 : 64, NSUB = BMQ / 64;
   constexpr bool kAcc = sizeof(T) == 2;  // dK/dV accumulators in AGPRs
   constexpr int KF = (D / 2) / MF::kK;
   constexpr int NDT = D / 32;
   constexpr int PF = 32 / MF::kK;
 
-  // two buffers x (Q tile, dO tile, lse[64], delta[64])
-  constexpr int BUF = 2 * G::BYTES + 2 * BMQ * 4;
+  // two buffers x (Q sub-tiles [NSUB], dO sub-tiles [NSUB], lse[BMQ], delta[BMQ])
+  constexpr int BUF = 2 * NSUB * G::BYTES + 2 * BMQ * 4;
   __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
@@ -386,19 +389,24 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   auto load_step = [&](int h, int qb0, char* buf) {
     const int64_t qoff = (int64_t)(b * p.Hq + h) * p.Sq;
     const uint32_t qbytes = (uint32_t)p.Sq * (uint32_t)G::RB;
-    dma.load(make_desc(static_cast<const T*>(p.q) + qoff * D, qbytes), qb0, buf);
-    dma.load(make_desc(static_cast<const T*>(p.dout) + qoff * D, qbytes), qb0, buf + G::BYTES);
+    const i32x4 qd = make_desc(static_cast<const T*>(p.q) + qoff * D, qbytes);
+    const i32x4 dd = make_desc(static_cast<const T*>(p.dout) + qoff * D, qbytes);
+#pragma unroll
+    for (int u = 0; u < NSUB; ++u) {
+      dma.load(qd, qb0 + 64 * u, buf + u * G::BYTES);
+      dma.load(dd, qb0 + 64 * u, buf + (NSUB + u) * G::BYTES);
+    }
     // Raw load only: a use here would make the wave wait (vmcnt(0)) for the
     // tile DMA just issued as well; the log2 scaling happens at the store.
-    // wave 0 stages lse, wave 1 delta (a wave-uniform choice: the pointer
-    // stays in scalar registers)
+    // The first BMQ/64 waves stage lse, the next BMQ/64 delta (a wave-uniform
+    // choice: the pointer stays in scalar registers).
     const int q = min(qb0 + (tid & (BMQ - 1)), p.Sq - 1);
-    if (wv_u < 2) lreg = (wv_u == 0 ? p.lse : p.delta)[qoff + q];
+    if (wv_u < 2 * NSUB) lreg = (wv_u < NSUB ? p.lse : p.delta)[qoff + q];
   };
   auto store_step = [&](char* buf, int qb0) {
     if (tid < 2 * BMQ) {
       const bool valid = qb0 + (tid & (BMQ - 1)) < p.Sq;
-      reinterpret_cast<float*>(buf + 2 * G::BYTES)[tid] = valid ? (tid < BMQ ? lreg * kLog2e : lreg) : 0.f;
+      reinterpret_cast<float*>(buf + 2 * NSUB * G::BYTES)[tid] = valid ? (tid < BMQ ? lreg * kLog2e : lreg) : 0.f;
     }
   };
 
@@ -581,7 +589,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   auto run = [&](auto masked, int st_end) {
     for (; st < st_end; ++st) {
       const char* buf = smem + (st & 1) * BUF;
-      const float* slse = reinterpret_cast<const float*>(buf + 2 * G::BYTES);
+      const float* slse = reinterpret_cast<const float*>(buf + 2 * NSUB * G::BYTES);
       int h_unused, qb0;
       coords(st, pos, h_unused, qb0);
       const Pos npos = advance(st, pos);
@@ -590,7 +598,11 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       if (has_next) coords(st + 1, npos, nh, nqb0);
       char* const nbuf = smem + ((st + 1) & 1) * BUF;
       if (has_next) load_step(nh, nqb0, nbuf);
-      step_body(masked, buf, buf + G::BYTES, slse, slse + BMQ, qb0);
+      // one copy of the sequence, run once per 64-row sub-step
+#pragma unroll 1
+      for (int u = 0; u < NSUB; ++u)
+        step_body(masked, buf + u * G::BYTES, buf + (NSUB + u) * G::BYTES, slse + 64 * u, slse + BMQ + 64 * u,
+                  qb0 + 64 * u);
       if (has_next) store_step(nbuf, nqb0);
       pos = npos;
       dma_wait();
