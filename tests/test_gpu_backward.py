@@ -99,11 +99,15 @@ def test_grads_head_dim_64_and_scale(dt):
         check_grad(g, w, dt, "d" + name)
 
 
-@pytest.mark.parametrize("Sq,Sk", [(64, 300), (300, 64)])
-def test_grads_sq_ne_sk_causal(Sq, Sk):
-    got, want, _ = _grads("f32", 1, 2, 1, Sq, Sk, True, seed=7)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("Sq,Sk", [(64, 300), (300, 64), (192, 192), (40, 200)])
+def test_grads_sq_ne_sk_causal(dt, Sq, Sk):
+    # top-left causal with Sq != Sk; 16-bit dK/dV steps cover 128 query rows
+    # as two 64-row passes: Sq = 192 (a last step with one valid pass) and
+    # Sq < 64 exercise the partially and fully invalid passes
+    got, want, _ = _grads(dt, 1, 2, 1, Sq, Sk, True, seed=7)
     for name, g, w in zip("qkv", got, want):
-        check_grad(g, w, "f32", "d" + name)
+        check_grad(g, w, dt, "d" + name)
 
 
 def test_value_and_grad_loss():
