@@ -26,7 +26,8 @@
 // the gfx950 transposing LDS load (ds_read_b64_tr_b16: within each 16-lane
 // group, lane i receives element [4t + i/4][i%4] of the 16 x 4 block the group
 // addressed, so lane j pointing at V[k0 + j/4][d0 + 4(j%4)] hands lane i the
-// values V[k0 + t][d0 + i]). For float32 V is staged transposed.
+// values V[k0 + t][d0 + i]). For float32 each lane reads its single V^T
+// element of an MFMA step straight from the row-major tile.
 // LDS tiles are unpadded with 16-byte chunks XOR-swizzled per row so the MFMA
 // reads and the staging writes are free of bank conflicts.
 //
