@@ -75,3 +75,117 @@ def test_sweep_backward(dt, D, B, Hq, Hkv, Sq, Sk, causal, kv_len, scale):
     if kv_len is not None:
         # keys at or past kv_len get exactly zero gradient
         assert (host(k.grad)[:, :, kv_len:] == 0).all() and (host(v.grad)[:, :, kv_len:] == 0).all()
+
+
+def _rope_cases(seed: int, n: int):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        dt = ("bf16", "f16", "f32")[i % 3]
+        D = (128, 64)[(i // 3) % 2]
+        Hkv = int(rng.integers(1, 3))
+        g = int(rng.choice([1, 2, 4]))
+        Sq = int(rng.integers(1, 260))
+        Sk = Sq if i % 2 == 0 else int(rng.integers(1, 260))
+        causal = bool(rng.integers(0, 2))
+        kv_len = int(rng.integers(1, Sk + 1)) if rng.integers(0, 2) else None
+        cases.append(pytest.param(dt, D, Hkv * g, Hkv, Sq, Sk, causal, kv_len, id=f"r{i}-{dt}-D{D}"))
+    return cases
+
+
+@pytest.mark.parametrize("dt,D,Hq,Hkv,Sq,Sk,causal,kv_len", _rope_cases(303, 12))
+def test_sweep_rope_forward_backward(dt, D, Hq, Hkv, Sq, Sk, causal, kv_len):
+    """Fused RoPE (separate K tables when Sq != Sk, fused_rope.py:154-160)
+    forward and its RoPE-aware backward vs the oracle."""
+    from oracle import rope_attention_bwd_ref, rope_attention_ref
+    from pallas_flash import flash_attention_rope, precompute_rope
+    note(f"sweep rope dt={dt} D={D} Hq={Hq} Hkv={Hkv} Sq={Sq} Sk={Sk} causal={causal} kv_len={kv_len}")
+    q, k, v, do = _inputs(13, dt, 1, Hq, Hkv, Sq, Sk, D)
+    cos, sin = precompute_rope(max(Sq, Sk), D, 10000.0, device="cuda")
+    qc, qs, kc, ks = cos[:Sq], sin[:Sq], cos[:Sk], sin[:Sk]
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    out = flash_attention_rope(q, k, v, qc, qs, kc, ks, causal=causal, kv_len=kv_len)
+    out.backward(do)
+    args = (host(q), host(k), host(v))
+    tabs = (host(qc), host(qs), host(kc), host(ks))
+    check_fwd(host(out), rope_attention_ref(*args, *tabs, causal=causal, kv_len=kv_len), dt)
+    want = rope_attention_bwd_ref(*args, host(do), *tabs, causal=causal, kv_len=kv_len)
+    for name, t, w in zip("qkv", (q, k, v), want):
+        check_grad(host(t.grad), w, dt, "d" + name)
+
+
+def _decode_cases(seed: int, n: int):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        dt = ("bf16", "f16", "f32")[i % 3]
+        D = (128, 64)[(i // 3) % 2]
+        Hkv = int(rng.integers(1, 4))
+        g = int(rng.choice([1, 2, 4, 8]))
+        B = int(rng.integers(1, 5))
+        cap = int(rng.integers(1, 700))
+        L = int(rng.integers(1, cap + 1))
+        cases.append(pytest.param(dt, D, B, Hkv * g, Hkv, cap, L, id=f"d{i}-{dt}-D{D}"))
+    return cases
+
+
+@pytest.mark.parametrize("dt,D,B,Hq,Hkv,cap,L", _decode_cases(404, 12))
+def test_sweep_decode(dt, D, B, Hq, Hkv, cap, L):
+    """Decode over the [0, L) prefix of a cache of `cap` slots whose tail is
+    NaN (test_decode.py:33, :38-49)."""
+    from oracle import decode_ref
+    from pallas_flash import flash_attention_decode
+    note(f"sweep decode dt={dt} D={D} B={B} Hq={Hq} Hkv={Hkv} cap={cap} L={L}")
+    rng = np.random.default_rng(14)
+    q = rng.standard_normal((B, Hq, 1, D))
+    k = rng.standard_normal((B, Hkv, cap, D))
+    v = rng.standard_normal((B, Hkv, cap, D))
+    k[:, :, L:] = np.nan
+    v[:, :, L:] = np.nan
+    tq, tk, tv = dev(q, dt), dev(k, dt), dev(v, dt)
+    out = host(flash_attention_decode(tq, tk, tv, L))
+    check_fwd(out, decode_ref(host(tq), host(tk), host(tv), L), dt)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_sweep_paged(seed):
+    """Paged decode over scrambled, partly shared pages with -1 padding past
+    each sequence's last page and NaN everywhere no valid row lives
+    (paged.py:119-121; test_paged.py:25-28, :61-91)."""
+    from oracle import paged_ref
+    from pallas_flash import paged_flash_attention
+    import torch
+    rng = np.random.default_rng(500 + seed)
+    dt = ("bf16", "f16", "f32")[seed % 3]
+    D = (128, 64)[(seed // 3) % 2]
+    Hkv = int(rng.integers(1, 4))
+    Hq = Hkv * int(rng.choice([1, 2, 4, 8]))
+    page = int(rng.choice([16, 32, 64, 128]))
+    B = int(rng.integers(1, 6))
+    lens = rng.integers(0, 5 * page + 1, B).astype(np.int32)
+    P = int(max(1, -(-int(lens.max()) // page)))
+    num_pages = B * P + 3
+    note(f"sweep paged dt={dt} D={D} B={B} Hq={Hq} Hkv={Hkv} page={page} lens={lens.tolist()}")
+    table = np.full((B, P), -1, np.int32)
+    perm = rng.permutation(num_pages)
+    used = 0
+    for b in range(B):
+        n = -(-int(lens[b]) // page)
+        table[b, :n] = perm[used:used + n]
+        used += n
+    if B > 1 and lens[0] > 0 and lens[1] > 0:
+        table[1, 0] = table[0, 0]  # a page shared by the first two sequences
+    # Rows no sequence reads stay NaN; a shared page gets the valid rows of
+    # both sequences (the later fill overwrites the earlier one's rows).
+    kp = np.full((num_pages, Hkv, page, D), np.nan)
+    vp = np.full((num_pages, Hkv, page, D), np.nan)
+    for b in range(B):
+        for j in range(-(-int(lens[b]) // page)):
+            rows = min(page, int(lens[b]) - j * page)
+            kp[table[b, j], :, :rows] = rng.standard_normal((Hkv, rows, D))
+            vp[table[b, j], :, :rows] = rng.standard_normal((Hkv, rows, D))
+    q = rng.standard_normal((B, Hq, 1, D))
+    tq, tk, tv = dev(q, dt), dev(kp, dt), dev(vp, dt)
+    out = host(paged_flash_attention(tq, tk, tv, torch.as_tensor(table), torch.as_tensor(lens)))
+    check_fwd(out, paged_ref(host(tq), host(tk), host(tv), table, lens), dt)
