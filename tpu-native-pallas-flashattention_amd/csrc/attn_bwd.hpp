@@ -160,8 +160,8 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
       Frag opnd[RING];
       Frag dsf[2];
       // The dP chains start at -delta (this lane's query), so they end as
-      // dP - delta and dS = P (dP - delta) needs no subtraction.
-      sx[0] = sx[1] = (f32x16)(0.f);
+      // dP - delta and dS = P (dP - delta) needs no subtraction; the S chains
+      // start from a literal zero (an inline constant of their first MFMA).
       dx[0] = dx[1] = (f32x16)(-dlt);
       // value r of half t: dS = P (dP - delta), pairs packed
       auto pds = [&](auto tc, int r) __attribute__((always_inline)) {
@@ -210,7 +210,7 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
           const Frag& a = opnd[g % RING];
           if constexpr (ph < 2) {
             if (k & 1) dx[ph] = MF::run(a, dof[k >> 1], dx[ph]);
-            else sx[ph] = MF::run(a, qf[k >> 1], sx[ph]);
+            else sx[ph] = MF::run(a, qf[k >> 1], k == 0 ? (f32x16)(0.f) : sx[ph]);
           } else {
             constexpr int t = ph - 2;
             if (k % NDT == 0) {
