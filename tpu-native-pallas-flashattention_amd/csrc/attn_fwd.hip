@@ -491,6 +491,11 @@ hipError_t launch_rope_rotate_k(const void* k, void* k_out, const float* cos, co
 
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream) {
+  if (p.rows_per_wave == 64) {
+    if (head_dim != 128) return hipErrorInvalidValue;
+    return launch_attn_fwd_w64(p, dtype, causal, rope, stream);
+  }
+  if (p.rows_per_wave != 32) return hipErrorInvalidValue;
   switch (dtype) {
     case kF32: return launch_dim<float>(p, head_dim, causal, rope, stream);
     case kBF16: return launch_dim<bf16_t>(p, head_dim, causal, rope, stream);

@@ -29,6 +29,18 @@ int check_attn_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, 
 
 int finish(hipError_t e) { return e == hipSuccess ? PF_OK : PF_ERR_LAUNCH; }
 
+// Query rows per wave of the forward kernel: 32 (attn_fwd.hip). The 64-row
+// tiling (attn_fwd_w64.hip: bf16/f16, D = 128, one wave per SIMD) is opt-in
+// with PF_FWD_ROWS_PER_WAVE=64: it halves the LDS reads per MFMA but measures
+// slower at the headline shapes (every barrier and every work item's
+// prologue and epilogue is exposed at one workgroup per CU).
+int fwd_rows_per_wave(const pf_attn_fwd_args* a) {
+  const bool wide_ok = a->dtype != PF_DTYPE_F32 && a->head_dim == 128;
+  if (!wide_ok) return 32;
+  const char* ov = getenv("PF_FWD_ROWS_PER_WAVE");
+  return (ov != nullptr && atoi(ov) == 64) ? 64 : 32;
+}
+
 int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   int st = check_attn_dims(a->batch, a->num_heads, a->num_kv_heads, a->seq_len_q, a->seq_len_k,
                            a->head_dim, a->kv_len, a->sm_scale, a->dtype);
@@ -51,7 +63,8 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   // A workgroup's 4 waves cover hpw query heads of one GQA group x rpw rows:
   // the K/V tiles it stages serve all of them.
   p->hpw = (p->g % 4 == 0) ? 4 : (p->g % 2 == 0) ? 2 : 1;
-  p->rpw = 128 / p->hpw;
+  p->rows_per_wave = fwd_rows_per_wave(a);
+  p->rpw = 4 * p->rows_per_wave / p->hpw;
   p->n_qblk = (a->seq_len_q + p->rpw - 1) / p->rpw;
   const int64_t n_work = (int64_t)a->batch * (a->num_heads / p->hpw) * p->n_qblk;
   if (n_work > kMaxGrid) return PF_ERR_UNSUPPORTED;

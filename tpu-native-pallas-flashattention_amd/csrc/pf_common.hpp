@@ -20,6 +20,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace pf {
 
 typedef __bf16 bf16_t;
@@ -218,6 +221,18 @@ __device__ inline float wave_xor32_max(float x) {
 __device__ inline float wave_xor32_sum(float x) {
   const f32x2 v = lane_pair(x);
   return v[0] + v[1];
+}
+
+// f(std::integral_constant<int, i>{}) for i = 0 .. N-1, each call inlined with
+// i a compile-time constant (a fully unrolled loop whose index can select
+// registers and `if constexpr` branches).
+template <typename F, int... I>
+__device__ __attribute__((always_inline)) inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __attribute__((always_inline)) inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // Workgroup -> work-item remap that keeps the `group` consecutive work items

@@ -19,14 +19,17 @@ struct FwdParams {
   const float* q_sin;
   int B, Hq, Hkv, Sq, Sk, kv_len, g;
   float scale_log2;  // sm_scale * log2(e)
+  int rows_per_wave; // 32 (attn_fwd.hip) or 64 (attn_fwd_w64.hip: 16-bit, D = 128)
   int hpw;           // query heads per workgroup (1, 2 or 4; divides g)
-  int rpw;           // query rows per head per workgroup (128 / hpw)
+  int rpw;           // query rows per head per workgroup (4 * rows_per_wave / hpw)
   int n_qblk;        // ceil(Sq / rpw)
   int n_work;        // B * Hq / hpw * n_qblk
 };
 
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream);
+// The 64-rows-per-wave forward (p.rows_per_wave == 64; bf16/f16, D = 128).
+hipError_t launch_attn_fwd_w64(const FwdParams& p, int dtype, bool causal, bool rope, hipStream_t stream);
 
 // Rotate rows [0, kv_len) of every (batch, head) of a [B, H, Sk, D] tensor
 // into k_out (same layout): x*cos + rotate_half(x)*sin with the [>= kv_len, D]
