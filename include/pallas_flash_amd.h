@@ -55,6 +55,10 @@ typedef enum { PF_DTYPE_F32 = 0, PF_DTYPE_BF16 = 1, PF_DTYPE_F16 = 2 } pf_dtype;
  *       lse = 0.
  *   kv_len in (0, seq_len_k]; keys >= kv_len are never read.
  *   causal: q_pos >= k_pos, top-left aligned (also when seq_len_q != seq_len_k).
+ * Environment: PF_FWD_ROWS_PER_WAVE=64 selects the 64-rows-per-wave kernel
+ * for bf16/f16 with head_dim 128 (same results, one workgroup per CU);
+ * unset or any other value keeps the default 32-row kernel. Also applies to
+ * pf_attn_fwd_rope.
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* q;
