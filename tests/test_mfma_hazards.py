@@ -1,0 +1,129 @@
+"""CPU tier: wait states after the inline-assembly MFMAs.
+
+The dK/dV kernel (MfmaAgpr) and the 64-row forward (MfmaVA, MfmaAgpr) issue
+32x32x16 MFMAs from inline assembly. The compiler's hazard recognizer cannot
+see inside the asm, so it adds no wait states before its own reads of the
+results -- including register copies it inserts on its own. The kernels
+route every such result through a tied s_nop fence; this test compiles the
+sources for gfx950 (as the Makefile does) and checks the assembly: no
+non-MFMA instruction may read or overwrite an MFMA destination register
+within 12 wait states of the MFMA (instructions count 1, s_nop k counts
+k + 1), and no MFMA may take a pending result as its A or B operand.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import re
+import shutil
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "tpu-native-pallas-flashattention_amd")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+NEED = 12
+
+SOURCES = {
+    "attn_fwd_w64.hip": [],
+    "attn_bwd_dkv16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+_REG = re.compile(r"([va])\[(\d+):(\d+)\]|([va])(\d+)$")
+
+
+def _regs(tok: str) -> set:
+    m = _REG.match(tok)
+    if not m:
+        return set()
+    if m.group(1):
+        return {(m.group(1), i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    return {(m.group(4), int(m.group(5)))}
+
+
+def scan(lines: list[str], need: int = NEED) -> list[str]:
+    """Early reads/overwrites of MFMA results in one kernel's assembly."""
+    found = []
+    for i, line in enumerate(lines):
+        s = line.strip()
+        if not s.startswith("v_mfma"):
+            continue
+        dst = _regs(s.split()[1].rstrip(","))
+        ws = 0
+        for j in range(i + 1, min(i + 400, len(lines))):
+            t = lines[j].strip()
+            if not t or t.startswith((";", ".")) or t.endswith(":"):
+                continue
+            if t.startswith(("s_cbranch", "s_branch", "s_endpgm", "s_setpc")) or ws >= need:
+                break
+            if t.startswith("s_nop"):
+                ws += int(t.split()[1]) + 1
+                continue
+            ws += 1
+            ops = [o.rstrip(",") for o in t.split()[1:]]
+            if t.startswith("v_mfma"):
+                ab = set().union(*[_regs(o) for o in ops[1:3]]) if len(ops) >= 3 else set()
+                if ab & dst:
+                    found.append(f"{s} -> {t} (A/B read after {ws} wait states)")
+                continue
+            rd = set().union(*[_regs(o) for o in ops[1:]]) if len(ops) > 1 else set()
+            wr = _regs(ops[0]) if ops else set()
+            if (rd | wr) & dst:
+                found.append(f"{s} -> {t} (after {ws} wait states)")
+                break
+    return found
+
+
+def _kernels(asm: str) -> dict[str, list[str]]:
+    out = {}
+    for m in re.finditer(r"^(_Z\S+):", asm, re.M):
+        end = asm.find(".Lfunc_end", m.end())
+        body = asm[m.end():end]
+        if "v_mfma" in body:
+            out[m.group(1)] = body.split("\n")
+    return out
+
+
+def _compile(src: str, extra: list[str], out_dir: str) -> str:
+    out = os.path.join(out_dir, src + ".s")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{os.path.join(ROOT, 'include')}", *extra, "--offload-device-only", "-S",
+           os.path.join(PKG, "csrc", src), "-o", out]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    with open(out) as f:
+        return f.read()
+
+
+@pytest.mark.skipif(not (os.path.exists(HIPCC) or shutil.which("hipcc")), reason="hipcc not available")
+def test_inline_asm_mfma_results_are_fenced():
+    with tempfile.TemporaryDirectory() as d, concurrent.futures.ThreadPoolExecutor(len(SOURCES)) as ex:
+        asms = dict(zip(SOURCES, ex.map(lambda kv: _compile(kv[0], kv[1], d), SOURCES.items())))
+    problems = []
+    n_kernels = 0
+    for src, asm in asms.items():
+        for name, body in _kernels(asm).items():
+            n_kernels += 1
+            problems += [f"{src} {name[:60]}: {p}" for p in scan(body)]
+    assert n_kernels >= 8, f"expected the MFMA kernels of {list(SOURCES)}, found {n_kernels}"
+    assert not problems, "\n".join(problems[:20])
+
+
+def test_scan_flags_an_early_read():
+    """The scan itself: a VALU read two instructions after an MFMA is
+    reported; the same read behind a 16-state fence is not."""
+    early = ["v_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], v[20:23], v[0:15]",
+             "v_mov_b32 v30, v31", "v_add_f32 v24, v3, v25"]
+    fenced = early[:1] + ["s_nop 7", "s_nop 7"] + early[1:]
+    copy = ["v_mfma_f32_32x32x16_bf16 a[0:15], v[16:19], v[20:23], a[0:15]", "v_accvgpr_mov_b32 a20, a15"]
+    chained = ["v_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], v[20:23], v[0:15]",
+               "v_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], v[20:23], v[0:15]"]
+    operand = ["v_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], v[20:23], v[0:15]",
+               "v_mfma_f32_32x32x16_bf16 v[32:47], v[0:3], v[20:23], v[32:47]"]
+    assert len(scan(early)) == 1
+    assert scan(fenced) == []
+    assert len(scan(copy)) == 1
+    assert scan(chained) == []          # srcC chaining on the same registers is interlocked
+    assert len(scan(operand)) == 1

@@ -93,6 +93,13 @@ __device__ inline float fmax3_raw(float a, float b, float c) {
 // slot 56, runs beside the first P.V MFMAs, which balances the VALU load of
 // the two phases.
 __host__ __device__ constexpr int exp_slot(int P) { return P < 24 ? 2 + (P * 26) / 24 : 32 + 2 * (P - 24); }
+// First pair whose stage A slot is >= slot (exp_slot is non-decreasing), so
+// the pairs whose stage A runs in slot s are [pair_lo(s), pair_lo(s + 1)).
+__host__ __device__ constexpr int pair_lo(int slot) {
+  int P = 0;
+  while (P < 32 && exp_slot(P) < slot) ++P;
+  return P;
+}
 
 // Fences for the results of the asm MFMAs above. The compiler cannot see
 // that those instructions write their outputs late, so any read it makes of
@@ -389,30 +396,36 @@ __global__ __launch_bounds__(256, 1) void pf_attn_fwd_w64_kernel(FwdParams p) {
         update_max(0, mxr[0]);
         update_max(1, mxr[1]);
       }
-      // exp / sum / pack of S_j, software-pipelined (exp_slot)
-      static_for<32>([&](auto pc) __attribute__((always_inline)) {
-        constexpr int P = decltype(pc)::value;
+      // exp / sum / pack of S_j, software-pipelined (exp_slot): stage st of
+      // the pairs whose stage A ran st slots ago
+      auto stage = [&](auto pc, auto stc) __attribute__((always_inline)) {
+        constexpr int P = decltype(pc)::value, st = decltype(stc)::value;
         constexpr int c = P >> 3, qt = (P >> 2) & 1, i = P & 3;
         constexpr int v = 8 * c + 2 * i, kt = v >> 4, r = v & 15;
-        constexpr int a = exp_slot(P);
-        if constexpr (m == a) {
+        if constexpr (st == 0) {
           ya[P][0] = fmaf(sc[kt][qt][r], c2, -m_run[qt]);
           ya[P][1] = fmaf(sc[kt][qt][r + 1], c2, -m_run[qt]);
           asm volatile("" : "+v"(ya[P][0]), "+v"(ya[P][1]));
-        } else if constexpr (m == a + 1) {
+        } else if constexpr (st == 1) {
           eb[P][0] = __builtin_amdgcn_exp2f(ya[P][0]);
           eb[P][1] = __builtin_amdgcn_exp2f(ya[P][1]);
           asm volatile("" : "+v"(eb[P][0]), "+v"(eb[P][1]));
-        } else if constexpr (m == a + 2) {
+        } else if constexpr (st == 2) {
           pw[P] = pack2<T>(eb[P][0], eb[P][1]);
           tc[P] = eb[P][0] + eb[P][1];
           asm volatile("" : "+v"(pw[P]), "+v"(tc[P]));
           if constexpr (i == 3)  // the 4 pairs of this (step, query tile) are packed
             pfr[qt][c] = __builtin_bit_cast(Frag, (u32x4){pw[P - 3], pw[P - 2], pw[P - 1], pw[P]});
-        } else if constexpr (m == a + 3) {
+        } else {
           rs[qt] += tc[P];
           asm volatile("" : "+v"(rs[qt]));
         }
+      };
+      static_for<4>([&](auto stc) __attribute__((always_inline)) {
+        constexpr int st = decltype(stc)::value;
+        if constexpr (m >= st)
+          static_for_range<pair_lo(m - st), pair_lo(m - st + 1)>(
+              [&](auto pc) __attribute__((always_inline)) { stage(pc, stc); });
       });
       if constexpr (m == 31) vfence4(sn[0][0], sn[0][1], sn[1][0], sn[1][1]);  // S_{j+1} is read from here on
       if constexpr (m >= 32) {

@@ -234,6 +234,15 @@ template <int N, typename F>
 __device__ __attribute__((always_inline)) inline void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
+// The same over i = LO .. HI-1 (empty when HI <= LO).
+template <int LO, typename F, int... I>
+__device__ __attribute__((always_inline)) inline void static_for_from(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, LO + I>{}), ...);
+}
+template <int LO, int HI, typename F>
+__device__ __attribute__((always_inline)) inline void static_for_range(F&& f) {
+  if constexpr (HI > LO) static_for_from<LO>(f, std::make_integer_sequence<int, HI - LO>{});
+}
 
 // Workgroup -> work-item remap that keeps the `group` consecutive work items
 // (the query heads of one GQA group) on one XCD. Workgroups are dispatched
