@@ -442,6 +442,10 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           dl[t][r4] = reinterpret_cast<const f32x4*>(sdl + 32 * hh + 16 * t)[r4];
         }
       uint32_t pw[2][8], dw[2][8];
+      Frag pf[2][2], df[2][2];
+      using H0 = std::integral_constant<int, 0>;
+      using H1 = std::integral_constant<int, 1>;
+      constexpr int NP = G::CPR;
       // value r of half t: P overwrites S and dS overwrites dP; pairs packed.
       auto pds = [&](auto tc, int r) {
         constexpr int t = decltype(tc)::value;
@@ -463,18 +467,70 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
         f[0] = __builtin_bit_cast(Frag, (u32x4){w[0], w[1], w[2], w[3]});
         f[1] = __builtin_bit_cast(Frag, (u32x4){w[4], w[5], w[6], w[7]});
       };
-      using H0 = std::integral_constant<int, 0>;
-      using H1 = std::integral_constant<int, 1>;
+      // D = 128 (one value per MFMA slot): the P/dS work of each value is
+      // software-pipelined over three slots -- FMA in slot NP (1 + t) + r,
+      // exp2 (and mask) one slot later, dS, the stores and the packing two
+      // slots later -- so no VALU op waits on a result of its own slot (at
+      // one wave per SIMD nothing else would fill that wait). The last values
+      // of a half finish in the first two slots of the next phase; their
+      // fragment (values 8..15) is first read 2 NDT slots into that phase.
+      constexpr bool kPipe = (G::CPR == 16);
+      float ya[2][16], pe[2][16];
+      auto stage = [&](auto tc, auto stc, int r) __attribute__((always_inline)) {
+        constexpr int t = decltype(tc)::value, st = decltype(stc)::value;
+        if constexpr (st == 0) {
+          ya[t][r] = fmaf(sx[t][r], p.scale_log2, -lv[t][r >> 2][r & 3]);
+          asm volatile("" : "+v"(ya[t][r]));
+        } else if constexpr (st == 1) {
+          float pv = __builtin_amdgcn_exp2f(ya[t][r]);
+          if constexpr (decltype(masked)::value) {
+            const int q = qb0 + 32 * hh + 16 * t + r;
+            const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
+            pv = ok ? pv : 0.f;
+          }
+          pe[t][r] = pv;
+          asm volatile("" : "+v"(pe[t][r]));
+        } else {
+          const float pv = pe[t][r];
+          const float ds = pv * dx[t][r];
+          sx[t][r] = pv;
+          dx[t][r] = ds;
+          if (r & 1) {
+            pw[t][r >> 1] = pack2<T>(sx[t][r - 1], pv);
+            dw[t][r >> 1] = pack2<T>(dx[t][r - 1], ds);
+            asm volatile("" : "+v"(pw[t][r >> 1]), "+v"(dw[t][r >> 1]));
+          }
+          if (r == 7) {
+            pf[t][0] = __builtin_bit_cast(Frag, (u32x4){pw[t][0], pw[t][1], pw[t][2], pw[t][3]});
+            df[t][0] = __builtin_bit_cast(Frag, (u32x4){dw[t][0], dw[t][1], dw[t][2], dw[t][3]});
+          } else if (r == 15) {
+            pf[t][1] = __builtin_bit_cast(Frag, (u32x4){pw[t][4], pw[t][5], pw[t][6], pw[t][7]});
+            df[t][1] = __builtin_bit_cast(Frag, (u32x4){dw[t][4], dw[t][5], dw[t][6], dw[t][7]});
+          }
+        }
+      };
+      // the pipelined stages of global slot j
+      auto pipe = [&](int j) __attribute__((always_inline)) {
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        const int r0 = j - NP, r1 = j - 2 * NP;  // value index of stage 0 per half
+        if (r0 >= 0 && r0 < 16) stage(H0{}, S0{}, r0);
+        if (r0 - 1 >= 0 && r0 - 1 < 16) stage(H0{}, S1{}, r0 - 1);
+        if (r0 - 2 >= 0 && r0 - 2 < 16) stage(H0{}, S2{}, r0 - 2);
+        if (r1 >= 0 && r1 < 16) stage(H1{}, S0{}, r1);
+        if (r1 - 1 >= 0 && r1 - 1 < 16) stage(H1{}, S1{}, r1 - 1);
+        if (r1 - 2 >= 0 && r1 - 2 < 16) stage(H1{}, S2{}, r1 - 2);
+      };
       // One fenced sequence of 4 phases x NP MFMAs (NP = CPR): S/dP half 0,
       // S/dP half 1, dV/dK half 0, dV/dK half 1. Operands are read LEAD MFMAs
       // ahead, across phase boundaries too.
-      constexpr int NP = G::CPR, NC = G::CPR / 2, LEAD = 2;
+      constexpr int NC = G::CPR / 2, LEAD = 2;
       constexpr int VPS = 16 / NP;  // P/dS values per MFMA slot
       typedef short v4i16 __attribute__((ext_vector_type(4)));
       const int rs0 = mfma_src_row(l32, 0), rs1 = mfma_src_row(l32, 1);
       const int sw0 = tile_swz<G::CPR>(rs0), sw1 = tile_swz<G::CPR>(rs1);
       Frag opnd[LEAD + 1];  // ring: operand of MFMA i in slot i % (LEAD + 1)
-      Frag pf[2][2], df[2][2];
       // The dP chains start at -delta (per query = per register), so they end
       // as dP - delta and dS = P (dP - delta) needs no subtraction.
       sx[0] = sx[1] = (f32x16)(0.f);
@@ -515,7 +571,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           if constexpr (ph < 2) {
             if (k & 1) dx[ph] = MF::run(a, vf[k >> 1], dx[ph]);
             else sx[ph] = MF::run(a, kf[k >> 1], sx[ph]);
-            if constexpr (ph == 1) {
+            if constexpr (ph == 1 && !kPipe) {
 #pragma unroll
               for (int e = 0; e < VPS; ++e) pds(H0{}, k * VPS + e);
             }
@@ -526,11 +582,12 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
             const Frag& bf = (k & 1) ? df[t][cc] : pf[t][cc];
             if constexpr (kAcc) MfmaAgpr<T>::run(acc, a, bf);
             else acc = MF::run(a, bf, acc);
-            if constexpr (ph == 2) {
+            if constexpr (ph == 2 && !kPipe) {
 #pragma unroll
               for (int e = 0; e < VPS; ++e) pds(H1{}, k * VPS + e);
             }
           }
+          if constexpr (kPipe) pipe(j);
           __builtin_amdgcn_sched_barrier(0);
         }
       };
@@ -539,11 +596,15 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       __builtin_amdgcn_sched_barrier(0);
       phase(std::integral_constant<int, 0>{});
       phase(std::integral_constant<int, 1>{});
-      frags(pw[0], pf[0]);
-      frags(dw[0], df[0]);
+      if constexpr (!kPipe) {
+        frags(pw[0], pf[0]);
+        frags(dw[0], df[0]);
+      }
       phase(std::integral_constant<int, 2>{});
-      frags(pw[1], pf[1]);
-      frags(dw[1], df[1]);
+      if constexpr (!kPipe) {
+        frags(pw[1], pf[1]);
+        frags(dw[1], df[1]);
+      }
       phase(std::integral_constant<int, 3>{});
     } else {
 #pragma unroll
