@@ -338,7 +338,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "step", "paged", "copy"], default="all")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
