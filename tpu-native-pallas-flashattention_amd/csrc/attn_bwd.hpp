@@ -429,8 +429,13 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   // one fenced MFMA sequence with LDS operands read two MFMAs ahead, in four
   // phases: S/dP half 0 | S/dP half 1 + P/dS VALU of half 0 |
   //   dV/dK of half 0 + P/dS VALU of half 1 | dV/dK of half 1.
-  auto step_body = [&](auto masked, const char* sq, const char* sdo, const float* slse, const float* sdl,
+  // 16-bit: operand ring of the fenced sequence, shared by the NSUB passes
+  // of a step so that the last slots of one pass can read the first operands
+  // of the next (its Q/dO sub-tiles are already resident).
+  typename MF::Frag opnd[3];
+  auto step_body = [&](auto masked, auto uc, const char* sq, const char* sdo, const float* slse, const float* sdl,
                        int qb0) {
+    constexpr int U = decltype(uc)::value;  // pass within the step
     f32x16 sx[2], dx[2];
     if constexpr (sizeof(T) == 2) {
       f32x4 lv[2][4], dl[2][4];
@@ -530,7 +535,10 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       typedef short v4i16 __attribute__((ext_vector_type(4)));
       const int rs0 = mfma_src_row(l32, 0), rs1 = mfma_src_row(l32, 1);
       const int sw0 = tile_swz<G::CPR>(rs0), sw1 = tile_swz<G::CPR>(rs1);
-      Frag opnd[LEAD + 1];  // ring: operand of MFMA i in slot i % (LEAD + 1)
+      static_assert(LEAD + 1 == 3, "ring size");
+      // MFMA i of pass U uses ring slot (ROFF + i) % 3: the index runs on
+      // across the passes of a step
+      constexpr int NT = 4 * NP, ROFF = (U * NT) % (LEAD + 1);
       // The dP chains start at -delta (per query = per register), so they end
       // as dP - delta and dS = P (dP - delta) needs no subtraction.
       sx[0] = sx[1] = (f32x16)(0.f);
@@ -538,13 +546,17 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dx[t][r] = -dl[t][r >> 2][r & 3];
+      // operand of MFMA i (i >= NT: MFMA i - NT of the next pass)
       auto read = [&](int i) __attribute__((always_inline)) {
-        const int ph = i / NP, k = i % NP;
+        const int slot = (ROFF + i) % (LEAD + 1);
+        const bool nx = i >= NT;
+        const int ii = nx ? i - NT : i;
+        const int ph = ii / NP, k = ii % NP;
         if (ph < 2) {
           // S/dP: k even = Q chunk k/2 (S chain), k odd = dO chunk k/2 (dP chain)
           const int r = ph ? rs1 : rs0, sw = ph ? sw1 : sw0;
-          const char* tile = (k & 1) ? sdo : sq;
-          opnd[i % (LEAD + 1)] = __builtin_bit_cast(Frag, lds16(tile + r * G::RB + 16 * ((hh * NC + (k >> 1)) ^ sw)));
+          const char* tile = ((k & 1) ? sdo : sq) + (nx ? G::BYTES : 0);
+          opnd[slot] = __builtin_bit_cast(Frag, lds16(tile + r * G::RB + 16 * ((hh * NC + (k >> 1)) ^ sw)));
         } else {
           // dV/dK: k even = dO^T (dV), k odd = Q^T (dK); m = k/2: step 2t + m/NDT, block m%NDT
           const int t = ph - 2, m = k >> 1, c = 2 * t + m / NDT, dt = m % NDT;
@@ -554,7 +566,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           for (int r = 0; r < 2; ++r)
             part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) v4i16*)(tile + ta.off[dt][r] + (8 * c + 4 * r) * G::RB));
-          opnd[i % (LEAD + 1)] =
+          opnd[slot] =
               __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
         }
       };
@@ -566,8 +578,8 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
 #pragma unroll
         for (int k = 0; k < NP; ++k) {
           const int j = ph * NP + k;
-          if (j + LEAD < 4 * NP) read(j + LEAD);
-          const Frag& a = opnd[j % (LEAD + 1)];
+          if (j + LEAD < NT || U + 1 < NSUB) read(j + LEAD);
+          const Frag& a = opnd[(ROFF + j) % (LEAD + 1)];
           if constexpr (ph < 2) {
             if (k & 1) dx[ph] = MF::run(a, vf[k >> 1], dx[ph]);
             else sx[ph] = MF::run(a, kf[k >> 1], sx[ph]);
@@ -591,8 +603,10 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           __builtin_amdgcn_sched_barrier(0);
         }
       };
+      if constexpr (U == 0) {  // later passes had theirs read by the previous one
 #pragma unroll
-      for (int i = 0; i < LEAD; ++i) read(i);
+        for (int i = 0; i < LEAD; ++i) read(i);
+      }
       __builtin_amdgcn_sched_barrier(0);
       phase(std::integral_constant<int, 0>{});
       phase(std::integral_constant<int, 1>{});
@@ -659,11 +673,12 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       if (has_next) coords(st + 1, npos, nh, nqb0);
       char* const nbuf = smem + ((st + 1) & 1) * BUF;
       if (has_next) load_step(nh, nqb0, nbuf);
-      // one copy of the sequence, run once per 64-row sub-step
-#pragma unroll 1
-      for (int u = 0; u < NSUB; ++u)
-        step_body(masked, buf + u * G::BYTES, buf + (NSUB + u) * G::BYTES, slse + 64 * u, slse + BMQ + 64 * u,
+      // one copy of the sequence per 64-row pass
+      static_for<NSUB>([&](auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+        step_body(masked, uc, buf + u * G::BYTES, buf + (NSUB + u) * G::BYTES, slse + 64 * u, slse + BMQ + 64 * u,
                   qb0 + 64 * u);
+      });
       if (has_next) store_step(nbuf, nqb0);
       pos = npos;
       dma_wait();
