@@ -22,11 +22,16 @@
 // the operand rings (VGPRs) fill the 512-entry register file, so the MFMA /
 // VALU overlap must come from one instruction stream. The block loop is one
 // fenced sequence of 64 MFMA slots per 64-key block:
-//   slots  0..31  S_{j+1} = K_{j+1} Q^T  | m update + exp/sum/pack of S_j
-//   slots 32..63  O^T += V_j^T P_j^T     | masked per-lane max of S_{j+1}
-// with every LDS operand read issued a few slots ahead of its MFMA -- also
+//   slots  0..31  S_{j+1} = K_{j+1} Q^T  | m update; exp/sum/pack of S_j
+//                                          for P.V steps 0-2
+//   slots 32..63  O^T += V_j^T P_j^T     | exp/sum/pack for step 3; per-lane
+//                                          max of S_{j+1}
+// The exp work is software-pipelined over consecutive slots (exp_slot), and
+// every LDS operand read is issued a few slots ahead of its MFMA -- also
 // across the two phases and across the barrier that ends the block, so that
-// no LDS latency bubble follows the barrier.
+// no LDS latency bubble follows the barrier. Blocks crossing the causal
+// diagonal or kv_len are masked after the sequence, with their max taken
+// again.
 //
 // LDS: 4 K buffers and 4 V buffers (128 KB). Iteration j stages V_{j+2} and
 // K_{j+4} by DMA and, before its closing barrier, waits only for the tiles
