@@ -1,7 +1,7 @@
 """GPU tier: the opt-in 64-rows-per-wave forward (PF_FWD_ROWS_PER_WAVE=64,
 bf16/f16, D = 128) against the float64 oracle, through the backward that
 consumes its O and LSE, with fused RoPE, and against the default 32-row
-kernel at a larger shape.
+kernel at larger shapes up to config 3's.
 
 The host reads the variable at every call, so setting it for one test routes
 exactly that test's forwards through the wide kernel.
@@ -84,13 +84,14 @@ def test_wide_rope(wide, dt, Sq, Sk, causal):
     check_fwd(host(out), want, dt)
 
 
-@pytest.mark.parametrize("causal", [True, False])
-def test_wide_matches_default_kernel(monkeypatch, causal):
+@pytest.mark.parametrize("B,Hq,Hkv,S,causal", [(1, 8, 2, 1536, True), (1, 8, 2, 1536, False),
+                                               (2, 16, 4, 8192, True)])  # last: config 3's shape
+def test_wide_matches_default_kernel(monkeypatch, B, Hq, Hkv, S, causal):
     """Both tilings compute each row with the same operations in the same
     order; they may differ only where a bf16 rounding of O flips (one ulp)."""
-    B, Hq, Hkv, S = 1, 8, 2, 1536
     note(f"wide vs default B={B} Hq={Hq} Hkv={Hkv} S={S} causal={causal}")
-    q, k, v, _ = _inputs(24, "bf16", B, Hq, Hkv, S, S)
+    g = torch.Generator(device="cuda").manual_seed(24)
+    q, k, v = (torch.randn((B, h, S, 128), generator=g, device="cuda").to(torch.bfloat16) for h in (Hq, Hkv, Hkv))
     res = {}
     for rows in ("32", "64"):
         monkeypatch.setenv("PF_FWD_ROWS_PER_WAVE", rows)
