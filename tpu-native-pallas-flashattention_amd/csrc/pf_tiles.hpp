@@ -291,9 +291,7 @@ __device__ inline void mfma_nat_il(const char* tile, int l32, int hh, const type
       s1 = MF::run(chunk_frag<T>(a1[k], 0), bf[k], s1);
       valu(2 * k + 1);
     }
-#ifndef PF_NO_FENCE
     __builtin_amdgcn_sched_barrier(0);
-#endif
   }
 }
 
@@ -325,87 +323,7 @@ __device__ inline void mfma_trn_il(const char* tile, const TrAddr<T, D>& ta,
       acc[k % NDT] = MF::run(af[k], bf[k / NDT], acc[k % NDT]);
       valu(k);
     }
-#ifndef PF_NO_FENCE
     __builtin_amdgcn_sched_barrier(0);
-#endif
-  }
-}
-
-// s += tile_a rows x bf_a and d += tile_b rows x bf_b for 32-row half t (as
-// mfma_nat_pair), the two chains alternating; NV = 2 * CPR / 2 (MFMA 2c is
-// chunk c of tile_a, 2c + 1 chunk c of tile_b).
-template <typename T, int D, int LEAD = 2, typename VF>
-__device__ inline void mfma_nat_pair_il(const char* tile_a, const typename Mfma32<T>::Frag* bf_a,
-                                        const char* tile_b, const typename Mfma32<T>::Frag* bf_b, int t,
-                                        int l32, int hh, f32x16& s, f32x16& d, VF&& valu) {
-  using MF = Mfma32<T>;
-  using G = Tile<T, D>;
-  static_assert(sizeof(T) == 2, "16-bit operands");
-  constexpr int NC = G::CPR / 2;
-  const int r = mfma_src_row(l32, t);
-  const int sw = tile_swz<G::CPR>(r);
-  const char* ba = tile_a + r * G::RB;
-  const char* bb = tile_b + r * G::RB;
-  u32x4 a[NC], b[NC];
-#pragma unroll
-  for (int c = 0; c < NC + LEAD; ++c) {
-    if (c < NC) {
-      const int off = 16 * ((hh * NC + c) ^ sw);
-      a[c] = lds16(ba + off);
-      b[c] = lds16(bb + off);
-    }
-    if (c >= LEAD) {
-      const int k = c - LEAD;
-      s = MF::run(chunk_frag<T>(a[k], 0), bf_a[k], s);
-      valu(2 * k);
-      d = MF::run(chunk_frag<T>(b[k], 0), bf_b[k], d);
-      valu(2 * k + 1);
-    }
-#ifndef PF_NO_FENCE
-    __builtin_amdgcn_sched_barrier(0);
-#endif
-  }
-}
-
-// acc_a[dt] += tile_a^T x bf_a and acc_b[dt] += tile_b^T x bf_b over steps
-// [C0, C1) (as mfma_trn; bf indexed by step - C0), the two products
-// alternating: MFMA i belongs to product i & 1, with m = i >> 1 giving step
-// C0 + m / NDT and column block m % NDT. NV = 2 * (C1 - C0) * NDT.
-// AGPR = true: accumulate with MfmaAgpr.
-template <typename T, int D, int C0, int C1, bool AGPR, int LEAD = 2, typename VF>
-__device__ inline void mfma_trn2_il(const char* tile_a, const typename Mfma32<T>::Frag* bf_a, f32x16* acc_a,
-                                    const char* tile_b, const typename Mfma32<T>::Frag* bf_b, f32x16* acc_b,
-                                    const TrAddr<T, D>& ta, VF&& valu) {
-  using MF = Mfma32<T>;
-  using G = Tile<T, D>;
-  using Frag = typename MF::Frag;
-  static_assert(sizeof(T) == 2, "16-bit operands");
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
-  constexpr int NDT = D / 32, NM = 2 * (C1 - C0) * NDT;
-  Frag af[NM];
-#pragma unroll
-  for (int i = 0; i < NM + LEAD; ++i) {
-    if (i < NM) {
-      const int m = i >> 1, c = C0 + m / NDT, dt = m % NDT;
-      const char* tile = (i & 1) ? tile_b : tile_a;
-      v4i16 part[2];
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-        part[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(tile + ta.off[dt][r] + (8 * c + 4 * r) * G::RB));
-      af[i] = __builtin_bit_cast(Frag, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
-    }
-    if (i >= LEAD) {
-      const int k = i - LEAD, m = k >> 1, cc = m / NDT, dt = m % NDT;
-      f32x16& acc = (k & 1) ? acc_b[dt] : acc_a[dt];
-      const Frag& bf = (k & 1) ? bf_b[cc] : bf_a[cc];
-      if constexpr (AGPR) MfmaAgpr<T>::run(acc, af[k], bf);
-      else acc = MF::run(af[k], bf, acc);
-      valu(k);
-    }
-#ifndef PF_NO_FENCE
-    __builtin_amdgcn_sched_barrier(0);
-#endif
   }
 }
 
