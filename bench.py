@@ -344,7 +344,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
-              f"--gpus {args.gpus}); see DESIGN.md for how the path would shard.", file=sys.stderr)
+              f"--gpus {args.gpus}). Prefill would shard over (batch, KV-head group) units with no "
+              f"exchange, decode and paged decode over sequences.", file=sys.stderr)
         sys.exit(2)
 
     import torch
