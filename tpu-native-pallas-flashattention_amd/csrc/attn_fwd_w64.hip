@@ -12,9 +12,10 @@
 // semantics and the same online-softmax arithmetic; only the tiling differs.
 //
 // Why a second tiling: with 32 query rows per wave every 16-byte K or V^T
-// operand a lane reads from LDS feeds exactly one 32x32x16 MFMA, and the LDS
-// read rate, not the matrix cores, bounds the loop (an MFMA + LDS-read probe
-// of that shape reaches 62% of peak at 2 workgroups per CU). Here each wave
+// operand a lane reads from LDS feeds exactly one 32x32x16 MFMA, and issuing
+// and waiting on those reads, not the matrix cores, bounds the loop (an MFMA
+// + LDS-read probe of that shape reaches 62% of peak at 2 workgroups per CU;
+// the LDS itself shows no back-pressure). Here each wave
 // owns two 32-row query tiles, so every K chunk and every V^T fragment read
 // feeds two MFMAs (the same probe: 77% of peak at 1 workgroup per CU).
 // The price is one wave per SIMD: 128 O accumulators (AGPRs), 64 Q registers
