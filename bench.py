@@ -24,6 +24,13 @@ Secondary figures in the same line (each timed with HIP events):
 
 Synthetic inputs: N(0,1) from torch's CUDA generator seeded 0 (config 5's
 lengths and page permutation from numpy's default_rng(0)), cast to bf16.
+
+CPU baselines (reported, not targets; the float32 numpy oracle, timed on this
+host's cores on a bounded sample of each workload): "cpu_baseline" for config
+3 forward+backward, and secondary.cpu_baselines for config 2 (fused RoPE),
+config 4 (decode, per sequence on the sliced prefix) and config 5 (paged,
+per sequence on the gathered pages). "cores" is the number of host cores
+this process may run on; "blas_threads" numpy's BLAS thread count.
 """
 
 from __future__ import annotations
@@ -148,7 +155,7 @@ def bench_rope(L, _lib, torch, iters):
         ev.mark(i, 1)
     torch.cuda.synchronize()
     ms = ev.mean_ms(0, 1)
-    return ms, fwd_flops(B, Hq, D, causal_pairs(S))
+    return ms, fwd_flops(B, Hq, D, causal_pairs(S)), {"q": q, "k": k, "v": v, "cos": cos, "sin": sin}
 
 
 def _decode_args_and_ws(L, _lib, torch, args, size_fn):
@@ -184,7 +191,7 @@ def bench_decode(L, _lib, torch, iters):
     assert torch.isfinite(o.float()).all(), "decode output not finite"
     nbytes = B * Hkv * kv_len * D * 2 * 2 + 2 * B * Hq * D * 2
     del ws
-    return ev.mean_ms(0, 1), nbytes
+    return ev.mean_ms(0, 1), nbytes, {"q": q, "k": kc, "v": vc, "kv_len": kv_len}
 
 
 def bench_decode_step(L, _lib, torch, iters):
@@ -271,7 +278,7 @@ def bench_paged(L, _lib, torch, iters):
     npg = -(-lens // page)
     nbytes = int(lens.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2 + 4 * int(npg.sum()) + 4 * B
     del ws
-    return ev.mean_ms(0, 1), nbytes
+    return ev.mean_ms(0, 1), nbytes, {"q": q, "k": kp, "v": vp, "table": table, "lens": lens}
 
 
 def bench_copy(torch, iters):
@@ -290,6 +297,17 @@ def bench_copy(torch, iters):
     return ev.mean_ms(0, 1), nbytes
 
 
+def _host_cores():
+    """Host cores this process may run on, and numpy's BLAS thread count."""
+    cores = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_info
+        blas = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        blas = 1
+    return cores, int(blas)
+
+
 def cpu_baseline(c3):
     """The float32 numpy restatement of the reference algorithm (oracle/),
     forward + backward on a bounded sample of config 3: batch 0 (16 query
@@ -297,11 +315,7 @@ def cpu_baseline(c3):
     FLOPs of the sample / wall time."""
     import torch
     from oracle import attention_bwd_ref, attention_ref
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = 1
+    cores, blas = _host_cores()
     S, D = c3["S"], c3["D"]
     h = c3["host"]
     f32 = lambda t: t.float().cpu().numpy()
@@ -315,10 +329,93 @@ def cpu_baseline(c3):
     attention_bwd_ref(q, k, v, do, causal=True, dtype=np.float32)
     dt = time.perf_counter() - t0
     flops = 3.5 * fwd_flops(1, q.shape[1], D, causal_pairs(S))
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "blas_threads": blas,
+            "kind": "port",
             "sample": f"numpy float32 restatement (oracle/attention.py) of reference.py + its "
                       f"backward, fwd+bwd of config 3 batch 0 (16 of 32 (b, h) heads) at "
-                      f"S={S}, {dt:.1f} s wall; BLAS threads={threads}, elementwise ops 1 thread"}
+                      f"S={S}, {dt:.1f} s wall; matmuls on {blas} BLAS threads, elementwise "
+                      f"ops on 1 thread, {cores} host cores available"}
+
+
+def cpu_baseline_rope(r, n_kv=4):
+    """Config 2 on the CPU: the oracle's fused-RoPE restatement (rotation in
+    float32, then naive attention) for batch 0, KV heads [0, n_kv) (4 query
+    heads each, of 128 (b, h) in all) at S=4096, causal. Credited FLOPs of
+    the sample / wall time (the oracle calls only; host copies untimed)."""
+    from oracle import rope_attention_ref
+    cores, blas = _host_cores()
+    f32 = lambda t: t.float().cpu().numpy()
+    cos, sin = f32(r["cos"]), f32(r["sin"])
+    g = r["q"].shape[1] // r["k"].shape[1]
+    S, D = r["q"].shape[2], r["q"].shape[3]
+    dt = 0.0
+    for h in range(n_kv):
+        q = f32(r["q"][0:1, h * g:(h + 1) * g])
+        k, v = f32(r["k"][0:1, h:h + 1]), f32(r["v"][0:1, h:h + 1])
+        t0 = time.perf_counter()
+        rope_attention_ref(q, k, v, cos, sin, causal=True, dtype=np.float32)
+        dt += time.perf_counter() - t0
+    flops = fwd_flops(1, n_kv * g, D, causal_pairs(S))
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "blas_threads": blas,
+            "kind": "port",
+            "sample": f"numpy float32 oracle (rope_attention_ref) on config 2 batch 0, kv heads "
+                      f"0-{n_kv - 1} ({n_kv * g} of 128 query heads) at S={S}, {dt:.2f} s"}
+
+
+def cpu_baseline_decode(d):
+    """Config 4 on the CPU, per sequence on the sliced prefix (the reference's
+    decode oracle, tests/test_decode.py:33): the float32 oracle over every
+    sequence's [0, kv_len) slots. Algorithmic (bf16) bytes / time (the oracle
+    calls only; host copies untimed)."""
+    from oracle import decode_ref
+    cores, blas = _host_cores()
+    L = d["kv_len"]
+    f32 = lambda t: t.float().cpu().numpy()
+    B, Hq, _, D = d["q"].shape
+    Hkv = d["k"].shape[1]
+    dt = 0.0
+    for b in range(B):
+        q, k, v = f32(d["q"][b:b + 1]), f32(d["k"][b:b + 1, :, :L]), f32(d["v"][b:b + 1, :, :L])
+        t0 = time.perf_counter()
+        decode_ref(q, k, v, L, dtype=np.float32)
+        dt += time.perf_counter() - t0
+    nbytes = B * (Hkv * L * D * 2 * 2 + 2 * Hq * D * 2)
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": cores, "blas_threads": blas,
+            "kind": "port",
+            "sample": f"numpy float32 oracle (decode_ref) per sequence on the sliced prefix, all "
+                      f"{B} config-4 sequences (kv_len {L}), {dt:.2f} s; bytes credited as the "
+                      f"GPU's (bf16 K/V once + q + o)"}
+
+
+def cpu_baseline_paged(pg):
+    """Config 5 on the CPU, per sequence on the gathered pages (the
+    reference's paged oracle, tests/test_paged.py:25-28): the float32 oracle
+    (paged_ref: gather, then attend) over every sequence. Algorithmic (bf16)
+    bytes / time (the oracle calls only; host copies untimed)."""
+    import torch
+    from oracle import paged_ref
+    cores, blas = _host_cores()
+    table, lens = pg["table"], pg["lens"]
+    page = pg["k"].shape[2]
+    B, Hq, _, D = pg["q"].shape
+    Hkv = pg["k"].shape[1]
+    f32 = lambda t: t.float().cpu().numpy()
+    dt = 0.0
+    for b in range(B):
+        n = -(-int(lens[b]) // page)
+        sel = torch.as_tensor(table[b, :n].astype(np.int64), device=pg["k"].device)
+        q, kp, vp = f32(pg["q"][b:b + 1]), f32(pg["k"][sel]), f32(pg["v"][sel])
+        sub = np.arange(n, dtype=np.int32)[None]  # the sequence's pages, gathered in order
+        t0 = time.perf_counter()
+        paged_ref(q, kp, vp, sub, lens[b:b + 1], dtype=np.float32)
+        dt += time.perf_counter() - t0
+    n_pages = int(sum(-(-int(x) // page) for x in lens))
+    nbytes = int(lens.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2 + 4 * n_pages + 4 * B
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": cores, "blas_threads": blas,
+            "kind": "port",
+            "sample": f"numpy float32 oracle (paged_ref) per sequence on its gathered pages, all "
+                      f"{B} config-5 sequences ({int(lens.sum())} tokens), {dt:.2f} s; bytes "
+                      f"credited as the GPU's"}
 
 
 def load_traffic(kernel: str, workload: str):
@@ -361,16 +458,25 @@ def main():
         c3 = bench_cfg3(L, _lib, torch, args.steps, args.warmup)
         sec["fwd_tflops"] = c3["F"] / (c3["kern_ms"]["pf_attn_fwd_kernel"] * 1e-3) / 1e12
         sec["kernel_ms"] = {k: round(v, 4) for k, v in c3["kern_ms"].items()}
+    cpu_sec = {}
     if args.only in ("all", "rope"):
         log("cfg2 rope ...")
-        ms, F = bench_rope(L, _lib, torch, iters)
+        ms, F, rin = bench_rope(L, _lib, torch, iters)
         sec["rope_tflops"] = F / (ms * 1e-3) / 1e12
         sec["rope_ms"] = ms
+        if not args.skip_cpu:
+            log("cpu baseline cfg2 ...")
+            cpu_sec["rope"] = cpu_baseline_rope(rin)
+        del rin
     if args.only in ("all", "decode"):
         log("cfg4 decode ...")
-        ms, nb = bench_decode(L, _lib, torch, iters)
+        ms, nb, din = bench_decode(L, _lib, torch, iters)
         sec["decode_gbs"] = nb / (ms * 1e-3) / 1e9
         sec["decode_ms"] = ms
+        if not args.skip_cpu:
+            log("cpu baseline cfg4 ...")
+            cpu_sec["decode"] = cpu_baseline_decode(din)
+        del din
     if args.only in ("all", "step"):
         log("cfg4-shape decode step ...")
         ms, nb = bench_decode_step(L, _lib, torch, iters)
@@ -378,9 +484,13 @@ def main():
         sec["decode_step_ms"] = ms
     if args.only in ("all", "paged"):
         log("cfg5 paged ...")
-        ms, nb = bench_paged(L, _lib, torch, iters)
+        ms, nb, pin = bench_paged(L, _lib, torch, iters)
         sec["paged_gbs"] = nb / (ms * 1e-3) / 1e9
         sec["paged_ms"] = ms
+        if not args.skip_cpu:
+            log("cpu baseline cfg5 ...")
+            cpu_sec["paged"] = cpu_baseline_paged(pin)
+        del pin
 
     if args.only == "copy":
         log("copy calibration ...")
@@ -421,6 +531,8 @@ def main():
         line["secondary"]["paged_frac_hbm"] = round(sec["paged_gbs"] / PEAK_HBM_GBS, 4)
     if "fwd_tflops" in sec:
         line["secondary"]["fwd_frac_mfma"] = round(sec["fwd_tflops"] / PEAK_BF16_TFLOPS, 4)
+    if cpu_sec:
+        line["secondary"]["cpu_baselines"] = cpu_sec
     print(json.dumps(line), flush=True)
 
 

@@ -17,7 +17,9 @@
  *  - Validation happens on the host before any HIP call; a rejected call
  *    enqueues nothing. After enqueueing, hipGetLastError() is checked and a
  *    launch failure is reported as PF_ERR_LAUNCH.
- *  - Thread safety: stateless and reentrant.
+ *  - Thread safety: reentrant. The only state is the process-wide tuning
+ *    (pf_set_tuning) and a per-device cache of the CU count and kernel
+ *    occupancy, filled once per device under std::call_once.
  *  - Data types: dtype tags PF_DTYPE_F32 / PF_DTYPE_BF16 / PF_DTYPE_F16 name
  *    the storage type of q/k/v/o (and do/dq/dk/dv); all arithmetic is float32
  *    (MFMA with float32 accumulation). LSE / delta are always float32.
@@ -55,10 +57,10 @@ typedef enum { PF_DTYPE_F32 = 0, PF_DTYPE_BF16 = 1, PF_DTYPE_F16 = 2 } pf_dtype;
  *       lse = 0.
  *   kv_len in (0, seq_len_k]; keys >= kv_len are never read.
  *   causal: q_pos >= k_pos, top-left aligned (also when seq_len_q != seq_len_k).
- * Environment: PF_FWD_ROWS_PER_WAVE=64 selects the 64-rows-per-wave kernel
- * for bf16/f16 with head_dim 128 (same results, one workgroup per CU);
- * unset or any other value keeps the default 32-row kernel. Also applies to
- * pf_attn_fwd_rope.
+ * Tuning: fwd_rows_per_wave = 64 (pf_set_tuning, or PF_FWD_ROWS_PER_WAVE=64
+ * in the environment at the first call) selects the 64-rows-per-wave kernel
+ * for bf16/f16 with head_dim 128 (same results, one workgroup per CU); the
+ * default 32 keeps the 32-row kernel. Also applies to pf_attn_fwd_rope.
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* q;
@@ -78,7 +80,10 @@ int pf_attn_fwd(const pf_attn_fwd_args* args, void* stream);
 /* ---------------------------------------------------------------------------
  * Fused-RoPE forward (no LSE). Replaces the `flash_attention_rope_fwd`
  * pallas_call (fused_rope.py:183-213, kernel :53-113). Rotation is
- * x*cos + rotate_half(x)*sin in float32. Q is rotated in registers inside the
+ * x*cos + rotate_half(x)*sin in float32; for bf16/f16 the rotated Q and K are
+ * rounded once to dtype before the matrix-core product (the reference keeps
+ * them float32 for a float32 dot, fused_rope.py:75-78; float32 inputs stay
+ * float32 here too). Q is rotated in registers inside the
  * attention kernel; K rows [0, kv_len) are rotated exactly once by a prologue
  * kernel into `workspace`, which the attention kernel then streams (the
  * reference re-rotates every K tile for every query head and query block).
@@ -103,11 +108,17 @@ int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * RoPE rotation of a [batch, heads, seq_len, head_dim] tensor, the rotation
- * the fused forward applies (rotate-half, fused_rope.py:43-50; model.py:54-67):
+ * the fused forward applies (rotate-half, fused_rope.py:43-50; model.py:54-67).
+ * With x1, x2 the two halves of a row and c1, c2, s1, s2 the halves of its
+ * table rows:
  *   inverse = 0: out = x*cos + rotate_half(x)*sin
- *   inverse = 1: out = x*cos - rotate_half(x)*sin   (the transpose rotation:
- *               the VJP of the forward one -- the RoPE-aware backward; the
- *               reference's fused kernel is forward-only, README.md:156-157)
+ *                (out1 = x1 c1 - x2 s1, out2 = x2 c2 + x1 s2)
+ *   inverse = 1: the transpose of that linear map, i.e. its VJP -- the
+ *                RoPE-aware backward (the reference's fused kernel is
+ *                forward-only, README.md:156-157):
+ *                out1 = x1 c1 + x2 s2, out2 = x2 c2 - x1 s1
+ *                (exact for any table; for precompute_rope's tables, whose
+ *                halves agree, it is x*cos - rotate_half(x)*sin)
  * Row s of every (batch, head) uses table row s; float32 arithmetic, one
  * rounding to dtype. x and out may alias.
  *   cos, sin [rope_len, head_dim] float32 with rope_len >= seq_len
@@ -198,7 +209,11 @@ int pf_attn_decode(const pf_attn_decode_args* args, void* stream);
  * Sequence b attends min(context_lens[b], pages_per_seq*page_size) tokens; a
  * non-positive length gives o = 0. Table entries at logical pages at or past
  * ceil(len / page_size) are never read (so -1 padding is legal); live entries
- * are clamped into [0, num_pages). page_size must be a multiple of 16.
+ * are clamped into [0, num_pages). Any page_size >= 1 is accepted (the
+ * reference has no restriction). bf16/f16 with head_dim 128 and page_size a
+ * multiple of 4 run the streaming kernel (each 4-row load stays inside one
+ * page); other page sizes, dtypes and head dims run the generic split-KV
+ * kernel, with the same results to rounding.
  * workspace: at least pf_paged_attn_workspace_size(args) bytes.
  * ------------------------------------------------------------------------- */
 typedef struct {
@@ -323,6 +338,33 @@ typedef struct {
 
 size_t pf_attn_decode_step_workspace_size(const pf_attn_decode_step_args* args);
 int pf_attn_decode_step(const pf_attn_decode_step_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Process-wide tuning of kernel variants and launch shapes. Every setting
+ * computes the same attention (to float rounding order). No counterpart in
+ * the reference, whose only tuning inputs are the static block_q / block_k
+ * arguments of its pallas_calls (flash_attention.py:479-490), which this
+ * build accepts and ignores. Initial values come from the environment, read
+ * once per process at the first launch or tuning call:
+ *   PF_FWD_ROWS_PER_WAVE  32 (default) or 64: query rows per wave of the
+ *                         16-bit head_dim-128 forward (64: one workgroup per
+ *                         CU, half the LDS reads per matrix-core op)
+ *   PF_DECODE_STAGES      2 (default) .. 4: LDS ring depth of the streaming
+ *                         decode / paged kernel
+ *   PF_DECODE_WAVES       0 (default: one per resident slot, queried once per
+ *                         device) or the persistent decode grid size
+ * pf_set_tuning replaces all three for later calls (PF_ERR_INVALID for values
+ * outside those ranges; launches already enqueued are unaffected). Safe to
+ * call from any thread.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int32_t fwd_rows_per_wave;
+  int32_t decode_stages;
+  int32_t decode_waves;
+} pf_tuning;
+
+int pf_get_tuning(pf_tuning* out);
+int pf_set_tuning(const pf_tuning* tuning);
 
 /* Library version string (static storage). */
 const char* pf_version(void);

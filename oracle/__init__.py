@@ -20,6 +20,7 @@ from .attention import (  # noqa: F401
     attention_bwd_ref,
     precompute_rope_ref,
     apply_rope_ref,
+    apply_rope_vjp_ref,
     rope_attention_ref,
     rope_attention_bwd_ref,
     decode_ref,

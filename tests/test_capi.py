@@ -120,6 +120,17 @@ def test_bwd_requires_buffers(L):
     assert L.pf_attn_bwd(a, None) == _lib.PF_ERR_INVALID
 
 
+@pytest.mark.parametrize("sq,sk", [(1 << 22, 8), (8, 1 << 22), (1 << 23, 1 << 23)])
+def test_bwd_rejects_sequences_past_32bit_offsets(L, sq, sk):
+    """The backward kernels address one head's rows with 32-bit byte offsets
+    (buffer descriptors): longer sequences are refused, never wrapped."""
+    a = _lib.BwdArgs(q=8, k=8, v=8, o=8, do_=8, lse=8, delta=8, dq=8, dk=8, dv=8, batch=1,
+                     num_heads=1, num_kv_heads=1, seq_len_q=sq, seq_len_k=sk, head_dim=128, kv_len=sk,
+                     causal=0, sm_scale=0.1, dtype=1)
+    for fn in (L.pf_attn_bwd, L.pf_attn_bwd_dkv, L.pf_attn_bwd_dq, L.pf_attn_bwd_delta):
+        assert fn(a, None) == _lib.PF_ERR_UNSUPPORTED
+
+
 def _dec(**over):
     base = dict(q=8, k_cache=8, v_cache=8, o=8, batch=64, num_heads=32, num_kv_heads=8,
                 cache_size=8192, head_dim=128, cache_len=6000, sm_scale=0.1, dtype=1,
@@ -256,3 +267,26 @@ def _rope_args(**over):
 ])
 def test_rope_rejects_on_host(L, over, status):
     assert L.pf_rope(_rope_args(**over), None) == status
+
+
+def test_tuning_round_trip_and_rejections(L):
+    """pf_get_tuning / pf_set_tuning: defaults (no PF_* variables in this
+    environment), out-of-range values refused without changing anything,
+    and the context manager restores the previous values."""
+    import os
+    if any(v in os.environ for v in ("PF_FWD_ROWS_PER_WAVE", "PF_DECODE_STAGES", "PF_DECODE_WAVES")):
+        pytest.skip("tuning variables set in this environment")
+    assert _lib.get_tuning() == {"fwd_rows_per_wave": 32, "decode_stages": 2, "decode_waves": 0}
+    for bad in (dict(fwd_rows_per_wave=48), dict(decode_stages=1), dict(decode_stages=5),
+                dict(decode_waves=-1)):
+        t = _lib.Tuning(**{**_lib.get_tuning(), **bad})
+        assert L.pf_set_tuning(ctypes.byref(t)) == _lib.PF_ERR_INVALID
+        assert _lib.get_tuning()["fwd_rows_per_wave"] == 32
+    assert L.pf_set_tuning(None) == _lib.PF_ERR_INVALID
+    assert L.pf_get_tuning(None) == _lib.PF_ERR_INVALID
+    with _lib.tuning(fwd_rows_per_wave=64, decode_waves=7) as t:
+        assert t == _lib.get_tuning() == {"fwd_rows_per_wave": 64, "decode_stages": 2, "decode_waves": 7}
+    assert _lib.get_tuning() == {"fwd_rows_per_wave": 32, "decode_stages": 2, "decode_waves": 0}
+    with pytest.raises(TypeError):
+        with _lib.tuning(block_q=64):
+            pass

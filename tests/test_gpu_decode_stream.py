@@ -6,12 +6,14 @@ all (batch, kv head, head slice) sequences. These cases pin the partition
 logic against the oracle (flash_attention.py:555-589 decode on the cache
 prefix; paged.py:45-99 via the gathered-pages oracle, test_paged.py:25-28):
 sequences finished inside one wave, sequences cut across several waves, waves
-spanning many short sequences (grid forced small through PF_DECODE_WAVES),
+spanning many short sequences (grid forced small through the decode_waves tuning),
 zero-length paged batches, page sizes that are and are not multiples of the
 32-key stage, GQA groups of 1..32 heads, and exact NaN-tail invariance.
 """
 
 from __future__ import annotations
+
+import contextlib
 
 import numpy as np
 import pytest
@@ -19,7 +21,7 @@ import torch
 
 from gpu_util import check_fwd, dev, host, note
 from oracle import decode_ref, paged_ref
-from pallas_flash import flash_attention_decode, paged_flash_attention
+from pallas_flash import _lib, flash_attention_decode, paged_flash_attention
 
 pytestmark = pytest.mark.gpu
 
@@ -27,13 +29,15 @@ WAVES = [None, 1, 3, 7, 50]
 
 
 @pytest.fixture
-def waves(monkeypatch):
+def waves():
+    """set_waves(w): route this test's decodes through a persistent grid of w
+    waves (None: one per resident slot) via the library's tuning."""
+    stack = contextlib.ExitStack()
+
     def set_waves(w):
-        if w is None:
-            monkeypatch.delenv("PF_DECODE_WAVES", raising=False)
-        else:
-            monkeypatch.setenv("PF_DECODE_WAVES", str(w))
-    yield set_waves
+        stack.enter_context(_lib.tuning(decode_waves=0 if w is None else w))
+    with stack:
+        yield set_waves
 
 
 @pytest.mark.parametrize("w", WAVES)

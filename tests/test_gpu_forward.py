@@ -44,6 +44,31 @@ def test_matches_reference_f32(shape, causal):
     assert max_abs(out, ref) < 2e-3  # the reference's own bound
 
 
+def test_baseline_config1_fp32_mha():
+    """BASELINE config 1, the reference's own fp32 parity case
+    (tests/test_flash_attention.py:33-41): fp32, non-causal, MHA B=1 H=8
+    S=512 D=128, q, k, v ~ N(0, 1) from np.random.default_rng(0) (in that
+    order). o and LSE within 1e-5 relative of the float64 oracle, and o within
+    the reference's own 2e-3 absolute bound."""
+    B, H, S, D = 1, 8, 512, 128
+    note("config 1: f32 MHA B=1 H=8 S=512 D=128 non-causal")
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((B, H, S, D))
+    k = rng.standard_normal((B, H, S, D))
+    v = rng.standard_normal((B, H, S, D))
+    tq, tk, tv = dev(q, "f32"), dev(k, "f32"), dev(v, "f32")
+    out = flash_attention(tq, tk, tv, causal=False)
+    o2, lse = flash_attention_with_lse(tq, tk, tv, causal=False)
+    torch.cuda.synchronize()
+    ref, ref_lse = attention_ref(host(tq), host(tk), host(tv), causal=False)
+    o_rel, lse_rel = rel_err(host(out), ref), rel_err(host(lse), ref_lse)
+    note(f"config 1: o rel {o_rel:.3e} (abs {max_abs(host(out), ref):.3e}), lse rel {lse_rel:.3e}")
+    assert o_rel <= 1e-5
+    assert lse_rel <= 1e-5
+    assert max_abs(host(out), ref) < 2e-3
+    assert torch.equal(out, o2)
+
+
 @pytest.mark.parametrize("n_heads,n_kv_heads", [(8, 2), (8, 1), (4, 4)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_grouped_query_attention(n_heads, n_kv_heads, causal):

@@ -1,9 +1,9 @@
-"""GPU tier: the opt-in 64-rows-per-wave forward (PF_FWD_ROWS_PER_WAVE=64,
+"""GPU tier: the opt-in 64-rows-per-wave forward (tuning fwd_rows_per_wave=64,
 bf16/f16, D = 128) against the float64 oracle, through the backward that
 consumes its O and LSE, with fused RoPE, and against the default 32-row
 kernel at larger shapes up to config 3's.
 
-The host reads the variable at every call, so setting it for one test routes
+The host reads the tuning at every call, so setting it around one test routes
 exactly that test's forwards through the wide kernel.
 """
 
@@ -15,14 +15,15 @@ import torch
 
 from gpu_util import check_fwd, check_grad, dev, host, note
 from oracle import attention_bwd_ref, attention_ref
-from pallas_flash import flash_attention, flash_attention_with_lse
+from pallas_flash import _lib, flash_attention, flash_attention_with_lse
 
 pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture
-def wide(monkeypatch):
-    monkeypatch.setenv("PF_FWD_ROWS_PER_WAVE", "64")
+def wide():
+    with _lib.tuning(fwd_rows_per_wave=64):
+        yield
 
 
 def _cases(seed: int, n: int):
@@ -86,7 +87,7 @@ def test_wide_rope(wide, dt, Sq, Sk, causal):
 
 @pytest.mark.parametrize("B,Hq,Hkv,S,causal", [(1, 8, 2, 1536, True), (1, 8, 2, 1536, False),
                                                (2, 16, 4, 8192, True)])  # last: config 3's shape
-def test_wide_matches_default_kernel(monkeypatch, B, Hq, Hkv, S, causal):
+def test_wide_matches_default_kernel(B, Hq, Hkv, S, causal):
     """Both tilings compute each row with the same operations in the same
     order; they may differ only where a bf16 rounding of O flips (one ulp)."""
     note(f"wide vs default B={B} Hq={Hq} Hkv={Hkv} S={S} causal={causal}")
@@ -94,9 +95,9 @@ def test_wide_matches_default_kernel(monkeypatch, B, Hq, Hkv, S, causal):
     q, k, v = (torch.randn((B, h, S, 128), generator=g, device="cuda").to(torch.bfloat16) for h in (Hq, Hkv, Hkv))
     res = {}
     for rows in ("32", "64"):
-        monkeypatch.setenv("PF_FWD_ROWS_PER_WAVE", rows)
-        o, lse = flash_attention_with_lse(q, k, v, causal=causal)
-        torch.cuda.synchronize()
+        with _lib.tuning(fwd_rows_per_wave=int(rows)):
+            o, lse = flash_attention_with_lse(q, k, v, causal=causal)
+            torch.cuda.synchronize()
         res[rows] = (o.float(), lse.clone())
     o32, l32 = res["32"]
     o64, l64 = res["64"]

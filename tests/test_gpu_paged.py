@@ -50,6 +50,53 @@ def test_paged_matches_contiguous(dt, batch, n_heads, n_kv_heads, page_size, con
         assert max_abs(host(out), ref) < 2e-3
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("page_size", [1, 5, 7])
+def test_paged_page_size_not_multiple_of_4(dt, page_size):
+    """16-bit D = 128 pools whose page size is not a multiple of 4 run the
+    generic split-KV kernel (the streaming kernel's 4-row loads need a page
+    boundary every 4 rows); the reference takes any page size (paged.py:
+    102-192). Scrambled table, -1 padding past the live pages, a zero and an
+    over-long length, and NaN in every page no sequence reads."""
+    batch, n_heads, n_kv_heads, dim = 4, 8, 2, 128
+    lens = np.array([1, 0, 3 * page_size + 2, 40 * page_size], np.int32)
+    pps = 24
+    num_pages = 4 * pps + 8
+    note(f"paged odd page dt={dt} page={page_size} lens={lens.tolist()}")
+    rng = np.random.default_rng(100 + page_size)
+    q = rng.standard_normal((batch, n_heads, 1, dim))
+    kp = rng.standard_normal((num_pages, n_kv_heads, page_size, dim))
+    vp = rng.standard_normal((num_pages, n_kv_heads, page_size, dim))
+    perm = rng.permutation(num_pages)
+    table = np.full((batch, pps), -1, np.int32)
+    used = np.zeros(num_pages, bool)
+    cur = 0
+    for b in range(batch):
+        n = min(-(-int(lens[b]) // page_size), pps)
+        table[b, :n] = perm[cur:cur + n]
+        used[perm[cur:cur + n]] = True
+        cur += n
+    tq, tk, tv = dev(q, dt), dev(kp, dt), dev(vp, dt)
+    tt, tl = torch.as_tensor(table), torch.as_tensor(lens)
+    out = paged_flash_attention(tq, tk, tv, tt, tl)
+    ref = paged_ref(host(tq), host(tk), host(tv), table, lens)
+    check_fwd(host(out), ref, dt)
+    assert not host(out)[1].any()  # zero length -> zeros
+    kn, vn = tk.clone(), tv.clone()
+    unused = torch.as_tensor(np.nonzero(~used)[0], device=tk.device)
+    kn[unused] = float("nan")
+    vn[unused] = float("nan")
+    for b in range(batch):  # rows past each length in its last live page
+        L = min(int(lens[b]), pps * page_size)
+        n = -(-L // page_size)
+        if n and L < n * page_size:
+            kn[int(table[b, n - 1]), :, L - (n - 1) * page_size:] = float("nan")
+            vn[int(table[b, n - 1]), :, L - (n - 1) * page_size:] = float("nan")
+    out_nan = paged_flash_attention(tq, kn, vn, tt, tl)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_nan)
+
+
 def test_pages_are_shareable():
     rng = np.random.default_rng(7)
     q1 = rng.standard_normal((1, 2, 1, 128))

@@ -110,14 +110,24 @@ def test_config2_fused_rope_full_size():
         half = D // 2
         return x * cos + torch.cat([-x[..., half:], x[..., :half]], dim=-1) * sin
 
-    worst = 0.0
+    worst, worst_rounded = 0.0, 0.0
     for b in range(B):
         for h in range(Hkv):
             sl = slice(h * g, (h + 1) * g)
-            o_r, _ = _attn_group(rot(q[b, sl]), rot(k[b, h]), v[b, h].float(), 1.0 / D ** 0.5, True)
+            qr, kr = rot(q[b, sl]), rot(k[b, h])
+            o_r, _ = _attn_group(qr, kr, v[b, h].float(), 1.0 / D ** 0.5, True)
             worst = max(worst, float((out[b, sl].float() - o_r).abs().max()))
-    note(f"scale cfg2 worst {worst:.3e}")
-    assert worst <= 2e-2
+            # the kernel's own rounding of the rotated q and k to bf16
+            o_b, _ = _attn_group(qr.bfloat16().float(), kr.bfloat16().float(), v[b, h].float(),
+                                 1.0 / D ** 0.5, True)
+            worst_rounded = max(worst_rounded, float((out[b, sl].float() - o_b).abs().max()))
+            del o_r, o_b
+    note(f"scale cfg2 worst {worst:.3e} (vs a reference with the rotated q, k rounded to bf16: "
+         f"{worst_rounded:.3e})")
+    # Measured 9.02e-3 against the float32 rotation of fused_rope.py:75-78
+    # (deterministic inputs and kernel); the bar keeps a third of headroom
+    # for reordered arithmetic, under the north star's 2e-2.
+    assert worst <= 1.2e-2
 
 
 def test_config4_decode_full_size():

@@ -458,15 +458,57 @@ def test_decode_step_rope_relative_position_invariance(rng):
 from oracle import rope_attention_bwd_ref  # noqa: E402
 
 
-@pytest.mark.parametrize("causal,Hq,Hkv,Sq,Sk,kv_len", [(True, 2, 1, 5, 5, None), (False, 4, 2, 3, 6, 5)])
-def test_rope_backward_matches_finite_differences(rng, causal, Hq, Hkv, Sq, Sk, kv_len):
+def _random_tables(rng, S, D):
+    """cos/sin tables of any values, the two halves of every row different
+    (flash_attention_rope accepts any [S, D] table, fused_rope.py:170-173)."""
+    c, s = rng.standard_normal((S, D)), rng.standard_normal((S, D))
+    assert np.abs(s[:, :D // 2] - s[:, D // 2:]).min() > 0
+    return c, s
+
+
+def test_rope_vjp_is_the_transpose_of_the_rotation(rng):
+    """apply_rope_vjp_ref == J^T g, with J built column by column from unit
+    vectors through apply_rope_ref, and the adjoint (dot-product) identity,
+    for random tables whose halves differ."""
+    from oracle import apply_rope_vjp_ref
+    S, D = 5, 8
+    cos, sin = _random_tables(rng, S, D)
+    for p in range(S):
+        J = np.stack([apply_rope_ref(np.eye(D)[j][None, None, None], cos[p:p + 1], sin[p:p + 1])[0, 0, 0]
+                      for j in range(D)], axis=1)  # J[:, j] = rotation of e_j
+        g = rng.standard_normal(D)
+        got = apply_rope_vjp_ref(g[None, None, None], cos[p:p + 1], sin[p:p + 1])[0, 0, 0]
+        np.testing.assert_allclose(got, J.T @ g, rtol=1e-13, atol=1e-13)
+    x, g = rng.standard_normal((2, 3, S, D)), rng.standard_normal((2, 3, S, D))
+    lhs = float((apply_rope_ref(x, cos, sin) * g).sum())
+    rhs = float((x * apply_rope_vjp_ref(g, cos, sin)).sum())
+    assert lhs == pytest.approx(rhs, rel=1e-12)
+    # with these tables the transpose is NOT the rotation with -sin (which is
+    # only right when sin[:, :D/2] == sin[:, D/2:], as in precompute_rope's)
+    wrong = apply_rope_ref(g, cos, -sin)
+    assert np.abs(wrong - apply_rope_vjp_ref(g, cos, sin)).max() > 1e-2
+    # precompute_rope tables: the two agree
+    pc, ps = precompute_rope_ref(S, D, 100.0)
+    np.testing.assert_allclose(apply_rope_ref(g, pc, -ps), apply_rope_vjp_ref(g, pc, ps), rtol=1e-13,
+                               atol=1e-13)
+
+
+@pytest.mark.parametrize("causal,Hq,Hkv,Sq,Sk,kv_len,tables", [
+    (True, 2, 1, 5, 5, None, "precompute"), (False, 4, 2, 3, 6, 5, "precompute"),
+    (True, 2, 1, 5, 5, None, "random"), (False, 4, 2, 3, 6, 5, "random")])
+def test_rope_backward_matches_finite_differences(rng, causal, Hq, Hkv, Sq, Sk, kv_len, tables):
     D = 6
     q, k, v = _qkv(rng, 1, Hq, Hkv, Sq, Sk, D)
     do = rng.standard_normal(q.shape)
-    qc, qs = precompute_rope_ref(Sq + 3, D, 50.0)
-    kc, ks = precompute_rope_ref(Sk + 3, D, 50.0)
-    qc, qs = qc[3:], qs[3:]          # query positions 3.. (decode-like offset)
-    kc, ks = kc[:Sk], ks[:Sk]
+    if tables == "precompute":
+        qc, qs = precompute_rope_ref(Sq + 3, D, 50.0)
+        kc, ks = precompute_rope_ref(Sk + 3, D, 50.0)
+        qc, qs = qc[3:], qs[3:]          # query positions 3.. (decode-like offset)
+        kc, ks = kc[:Sk], ks[:Sk]
+    else:
+        qc, qs = _random_tables(rng, Sq, D)
+        kc, ks = _random_tables(rng, Sk, D)
+        qc, qs, kc, ks = 0.5 * qc, 0.5 * qs, 0.5 * kc, 0.5 * ks
     kw = dict(causal=causal, kv_len=kv_len, sm_scale=0.6)
     dq, dk, dv = rope_attention_bwd_ref(q, k, v, do, qc, qs, kc, ks, **kw)
 

@@ -405,16 +405,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 
 // Row rotation: the K prologue of the fused-RoPE forward and pf_rope. Each
 // thread rotates one 16-byte chunk of the first half of a row together with
-// its partner chunk D/2 further (x*cos + rotate_half(x)*sin in float32,
-// fused_rope.py:43-50, :75-78; sgn = -1 gives the transpose rotation
-// x*cos - rotate_half(x)*sin, the VJP of the forward one), then rounds once
-// to T. Row `pos` of each (b, h) uses table row `pos`; rows at or past
-// kv_len are not touched (the attention kernel never reads them).
-template <typename T, int D>
+// its partner chunk D/2 further, then rounds once to T. Row `pos` of each
+// (b, h) uses table row `pos`; rows at or past kv_len are not touched (the
+// attention kernel never reads them). With halves x1 = x[:D/2], x2 = x[D/2:]
+// and table halves c1, c2, s1, s2 of row pos:
+//   forward (fused_rope.py:43-50, :75-78: x*cos + rotate_half(x)*sin)
+//     y1 = x1 c1 - x2 s1,  y2 = x2 c2 + x1 s2;
+//   inverse = the transpose of that linear map (the VJP of the forward one,
+//   exact for any table, also when the halves of a table row differ)
+//     y1 = x1 c1 + x2 s2,  y2 = x2 c2 - x1 s1.
+template <typename T, int D, bool INVERSE>
 __global__ __launch_bounds__(256) void pf_rope_rotate_k_kernel(const T* __restrict__ k, T* __restrict__ out,
                                                                const float* __restrict__ cosb,
                                                                const float* __restrict__ sinb, int Sk,
-                                                               int kv_len, int64_t n_items, float sgn) {
+                                                               int kv_len, int64_t n_items) {
   constexpr int EPC = 16 / (int)sizeof(T);
   constexpr int HC = D / 2 / EPC;  // chunks per half row
   const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -432,8 +436,13 @@ __global__ __launch_bounds__(256) void pf_rope_rotate_k_kernel(const T* __restri
   const float* sn = sinb + (int64_t)pos * D + pc * EPC;
 #pragma unroll
   for (int e = 0; e < EPC; ++e) {
-    ra[e] = a[e] * cs[e] - sgn * (bb[e] * sn[e]);
-    rb[e] = bb[e] * cs[D / 2 + e] + sgn * (a[e] * sn[D / 2 + e]);
+    if constexpr (INVERSE) {
+      ra[e] = a[e] * cs[e] + bb[e] * sn[D / 2 + e];
+      rb[e] = bb[e] * cs[D / 2 + e] - a[e] * sn[e];
+    } else {
+      ra[e] = a[e] * cs[e] - bb[e] * sn[e];
+      rb[e] = bb[e] * cs[D / 2 + e] + a[e] * sn[D / 2 + e];
+    }
   }
   T* dst = out + row * D + pc * EPC;
   stg16(dst, f32_to_chunk<T>(ra));
@@ -462,12 +471,17 @@ hipError_t launch_dim(const FwdParams& p, int head_dim, bool causal, bool rope, 
 
 template <typename T, int D>
 hipError_t rotate_typed(const void* k, void* out, const float* cs, const float* sn, int B, int Hkv, int Sk,
-                        int kv_len, float sgn, hipStream_t st) {
+                        int kv_len, bool inverse, hipStream_t st) {
   constexpr int HC = D / 2 / (16 / (int)sizeof(T));
   const int64_t n_items = (int64_t)B * Hkv * kv_len * HC;
   if (n_items == 0) return hipSuccess;
-  hipLaunchKernelGGL((pf_rope_rotate_k_kernel<T, D>), dim3((unsigned)((n_items + 255) / 256)), dim3(256), 0,
-                     st, static_cast<const T*>(k), static_cast<T*>(out), cs, sn, Sk, kv_len, n_items, sgn);
+  const dim3 grid((unsigned)((n_items + 255) / 256)), block(256);
+  if (inverse)
+    hipLaunchKernelGGL((pf_rope_rotate_k_kernel<T, D, true>), grid, block, 0, st, static_cast<const T*>(k),
+                       static_cast<T*>(out), cs, sn, Sk, kv_len, n_items);
+  else
+    hipLaunchKernelGGL((pf_rope_rotate_k_kernel<T, D, false>), grid, block, 0, st, static_cast<const T*>(k),
+                       static_cast<T*>(out), cs, sn, Sk, kv_len, n_items);
   return hipGetLastError();
 }
 
@@ -476,15 +490,15 @@ hipError_t rotate_typed(const void* k, void* out, const float* cs, const float* 
 hipError_t launch_rope_rotate_k(const void* k, void* k_out, const float* cos, const float* sin, int B,
                                 int Hkv, int Sk, int kv_len, int dtype, int head_dim, hipStream_t stream,
                                 bool inverse) {
-  const float sgn = inverse ? -1.f : 1.f;
+  const bool inv = inverse;
   if (head_dim == 128) {
-    if (dtype == kF32) return rotate_typed<float, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, sgn, stream);
-    if (dtype == kBF16) return rotate_typed<bf16_t, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, sgn, stream);
-    if (dtype == kF16) return rotate_typed<f16_t, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, sgn, stream);
+    if (dtype == kF32) return rotate_typed<float, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
+    if (dtype == kBF16) return rotate_typed<bf16_t, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
+    if (dtype == kF16) return rotate_typed<f16_t, 128>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
   } else if (head_dim == 64) {
-    if (dtype == kF32) return rotate_typed<float, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, sgn, stream);
-    if (dtype == kBF16) return rotate_typed<bf16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, sgn, stream);
-    if (dtype == kF16) return rotate_typed<f16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, sgn, stream);
+    if (dtype == kF32) return rotate_typed<float, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
+    if (dtype == kBF16) return rotate_typed<bf16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
+    if (dtype == kF16) return rotate_typed<f16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
   }
   return hipErrorInvalidValue;
 }

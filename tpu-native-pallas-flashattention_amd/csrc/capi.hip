@@ -5,10 +5,40 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "../../include/pallas_flash_amd.h"
 #include "pf_kernels.hpp"
 
 namespace {
+
+// Process-wide tuning (pf_get_tuning / pf_set_tuning). The environment is read
+// once, at the first call that needs a value; afterwards every launch reads
+// three atomics and makes no environment or device query of its own.
+struct Tuning {
+  std::atomic<int> fwd_rows_per_wave{32};
+  std::atomic<int> decode_stages{2};
+  std::atomic<int> decode_waves{0};
+};
+
+bool tuning_valid(int rows, int stages, int waves) {
+  return (rows == 32 || rows == 64) && stages >= 2 && stages <= 4 && waves >= 0;
+}
+
+Tuning& tuning() {
+  static Tuning t;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    const char* r = getenv("PF_FWD_ROWS_PER_WAVE");
+    const char* s = getenv("PF_DECODE_STAGES");
+    const char* w = getenv("PF_DECODE_WAVES");
+    if (r != nullptr && atoi(r) == 64) t.fwd_rows_per_wave = 64;
+    if (s != nullptr && atoi(s) >= 2 && atoi(s) <= 4) t.decode_stages = atoi(s);
+    if (w != nullptr && atoi(w) > 0) t.decode_waves = atoi(w);
+  });
+  return t;
+}
 
 bool dtype_ok(int32_t d) { return d == PF_DTYPE_F32 || d == PF_DTYPE_BF16 || d == PF_DTYPE_F16; }
 bool head_dim_ok(int32_t d) { return d == 64 || d == 128; }
@@ -31,14 +61,13 @@ int finish(hipError_t e) { return e == hipSuccess ? PF_OK : PF_ERR_LAUNCH; }
 
 // Query rows per wave of the forward kernel: 32 (attn_fwd.hip). The 64-row
 // tiling (attn_fwd_w64.hip: bf16/f16, D = 128, one wave per SIMD) is opt-in
-// with PF_FWD_ROWS_PER_WAVE=64: it halves the LDS reads per MFMA but measures
-// slower at the headline shapes (every barrier and every work item's
-// prologue and epilogue is exposed at one workgroup per CU).
+// through the tuning (fwd_rows_per_wave = 64): it halves the LDS reads per
+// MFMA but measures slower at the headline shapes (every barrier and every
+// work item's prologue and epilogue is exposed at one workgroup per CU).
 int fwd_rows_per_wave(const pf_attn_fwd_args* a) {
   const bool wide_ok = a->dtype != PF_DTYPE_F32 && a->head_dim == 128;
   if (!wide_ok) return 32;
-  const char* ov = getenv("PF_FWD_ROWS_PER_WAVE");
-  return (ov != nullptr && atoi(ov) == 64) ? 64 : 32;
+  return tuning().fwd_rows_per_wave.load(std::memory_order_relaxed) == 64 ? 64 : 32;
 }
 
 int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
@@ -79,6 +108,25 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
 extern "C" {
 
 const char* pf_version(void) { return "pallas_flash_amd 0.1.0 (gfx950)"; }
+
+int pf_get_tuning(pf_tuning* out) {
+  if (!out) return PF_ERR_INVALID;
+  Tuning& t = tuning();
+  out->fwd_rows_per_wave = t.fwd_rows_per_wave.load();
+  out->decode_stages = t.decode_stages.load();
+  out->decode_waves = t.decode_waves.load();
+  return PF_OK;
+}
+
+int pf_set_tuning(const pf_tuning* in) {
+  if (!in || !tuning_valid(in->fwd_rows_per_wave, in->decode_stages, in->decode_waves))
+    return PF_ERR_INVALID;
+  Tuning& t = tuning();
+  t.fwd_rows_per_wave = in->fwd_rows_per_wave;
+  t.decode_stages = in->decode_stages;
+  t.decode_waves = in->decode_waves;
+  return PF_OK;
+}
 
 int pf_attn_fwd(const pf_attn_fwd_args* a, void* stream) {
   if (!a) return PF_ERR_INVALID;
@@ -157,6 +205,11 @@ static int fill_bwd(const pf_attn_bwd_args* a, pf::BwdParams* p, bool need_grads
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
   const int64_t rows = (int64_t)a->batch * a->num_heads * a->seq_len_q;
   if (rows > kMaxGrid) return PF_ERR_UNSUPPORTED;
+  // Per-(batch, head) byte offsets and buffer sizes are 32-bit inside the
+  // kernels (Q/dO rows of one query head, K/V rows of one kv head), as in
+  // the forward.
+  const int64_t max_rows = a->seq_len_q > a->seq_len_k ? a->seq_len_q : a->seq_len_k;
+  if ((max_rows + 256) * a->head_dim * 4 > 0x7fffffff) return PF_ERR_UNSUPPORTED;
   return PF_OK;
 }
 
@@ -219,17 +272,16 @@ static int decode_chunk(int64_t units, int max_len) {
 }
 
 // Streaming kernel (decode_stream.hip): a persistent grid of one-wave
-// workgroups, as many as are resident at once, with an LDS ring of 2 stages
-// (measured on MI355X: 2 stages x 4 waves per CU beat 3 x 3 and 4 x 2).
-// Tuning and test overrides: PF_DECODE_STAGES (2..4) and PF_DECODE_WAVES
-// (grid size; any value >= 1 is correct, only the resident count is fast).
+// workgroups, as many as are resident at once (queried once per device),
+// with an LDS ring of 2 stages (measured on MI355X: 2 stages x 4 waves per
+// CU beat 3 x 3 and 4 x 2). Tuning and test overrides: decode_stages (2..4)
+// and decode_waves (grid size; any value >= 1 is correct, only the resident
+// count is fast).
 static int stream_setup(pf::DecodeParams* p, int group) {
-  const char* env = getenv("PF_DECODE_STAGES");
-  int ns = env ? atoi(env) : 2;
-  if (ns < 2 || ns > 4) ns = 2;
+  Tuning& t = tuning();
+  const int ns = t.decode_stages.load(std::memory_order_relaxed);
   p->stages = ns;
-  const char* wenv = getenv("PF_DECODE_WAVES");
-  const int wv = wenv ? atoi(wenv) : 0;
+  const int wv = t.decode_waves.load(std::memory_order_relaxed);
   p->n_waves = wv > 0 ? wv : pf::decode_stream_waves(ns, group);
   p->n_split = 0;
   p->chunk = 0;

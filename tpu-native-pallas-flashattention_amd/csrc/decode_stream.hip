@@ -47,6 +47,8 @@
 #include "pf_common.hpp"
 #include "pf_kernels.hpp"
 
+#include <mutex>
+
 namespace pf {
 
 namespace {
@@ -552,24 +554,50 @@ bool decode_stream_supported(int dtype, int head_dim, bool paged, int page_size)
 }
 
 // Resident one-wave workgroups of the streaming kernel on the current device
-// (the persistent grid size). Without a usable device (a host-only query),
-// MI355X's 256 CUs and the LDS-limited occupancy are assumed.
+// (the persistent grid size). The device's CU count and the kernel's
+// occupancy for every (stages, query rows) variant are queried once per
+// device (std::call_once) and cached; later calls cost one hipGetDevice.
+// Without a usable device (a host-only query), MI355X's 256 CUs and the
+// LDS-limited occupancy are assumed.
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct StreamOccupancy {
+  std::once_flag once;
+  int cus = 0;
+  int per_cu[3][2] = {};  // [stages - 2][query rows 4 / 16]
+};
+StreamOccupancy g_occupancy[kMaxDevices];
+
+void query_occupancy(StreamOccupancy* o, int dev) {
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return;
+  o->cus = cus;
+  o->per_cu[0][0] = blocks_per_cu<2, 4>();
+  o->per_cu[0][1] = blocks_per_cu<2, 16>();
+  o->per_cu[1][0] = blocks_per_cu<3, 4>();
+  o->per_cu[1][1] = blocks_per_cu<3, 16>();
+  o->per_cu[2][0] = blocks_per_cu<4, 4>();
+  o->per_cu[2][1] = blocks_per_cu<4, 16>();
+}
+
+}  // namespace
+
 int decode_stream_waves(int stages, int group) {
   const bool small = group <= 4;
-  int per_cu = 0;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) == hipSuccess &&
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) {
-    switch (stages) {
-      case 3: per_cu = small ? blocks_per_cu<3, 4>() : blocks_per_cu<3, 16>(); break;
-      case 4: per_cu = small ? blocks_per_cu<4, 4>() : blocks_per_cu<4, 16>(); break;
-      default: per_cu = small ? blocks_per_cu<2, 4>() : blocks_per_cu<2, 16>(); break;
-    }
-  } else {
-    cus = 256;
+  const int si = (stages >= 2 && stages <= 4) ? stages - 2 : 0;
+  int per_cu = 0, cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+    StreamOccupancy& o = g_occupancy[dev];
+    std::call_once(o.once, query_occupancy, &o, dev);
+    cus = o.cus;
+    per_cu = o.per_cu[si][small ? 0 : 1];
   }
+  if (cus <= 0) cus = 256;
   if (per_cu <= 0) {
-    const int lds = stages * (2 * kTileB + (small ? 4 : 16) * kRowB);
+    const int lds = (si + 2) * (2 * kTileB + (small ? 4 : 16) * kRowB);
     per_cu = 160 * 1024 / lds;
   }
   return cus * max(per_cu, 1);

@@ -6,9 +6,10 @@ the library is missing or fails to load, every entry point raises.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
-from typing import Optional
+from typing import Iterator, Optional
 
 import torch
 
@@ -113,6 +114,10 @@ class DecodeStepArgs(ctypes.Structure):
     ]
 
 
+class Tuning(ctypes.Structure):
+    _fields_ = [("fwd_rows_per_wave", c_i32), ("decode_stages", c_i32), ("decode_waves", c_i32)]
+
+
 # (symbol, argtypes, restype) for every entry point the header declares.
 SIGNATURES = {
     "pf_attn_fwd": ([ctypes.POINTER(FwdArgs), c_ptr], ctypes.c_int),
@@ -131,6 +136,8 @@ SIGNATURES = {
     "pf_paged_cache_write": ([ctypes.POINTER(PagedWriteArgs), c_ptr], ctypes.c_int),
     "pf_attn_decode_step_workspace_size": ([ctypes.POINTER(DecodeStepArgs)], ctypes.c_size_t),
     "pf_attn_decode_step": ([ctypes.POINTER(DecodeStepArgs), c_ptr], ctypes.c_int),
+    "pf_get_tuning": ([ctypes.POINTER(Tuning)], ctypes.c_int),
+    "pf_set_tuning": ([ctypes.POINTER(Tuning)], ctypes.c_int),
     "pf_version": ([], ctypes.c_char_p),
 }
 
@@ -196,3 +203,29 @@ def require_device(*tensors: torch.Tensor) -> None:
                 f"got a tensor on {t.device}")
         if t.device != dev:
             raise ValueError(f"all tensors must be on one device, got {dev} and {t.device}")
+
+
+def get_tuning() -> dict:
+    """The library's process-wide tuning (pf_get_tuning)."""
+    t = Tuning()
+    check(lib().pf_get_tuning(ctypes.byref(t)), "pf_get_tuning")
+    return {name: getattr(t, name) for name, _ in Tuning._fields_}
+
+
+@contextlib.contextmanager
+def tuning(**overrides) -> Iterator[dict]:
+    """Run a block with some tuning fields replaced (pf_set_tuning), restoring
+    the previous values afterwards. Fields: fwd_rows_per_wave (32 | 64),
+    decode_stages (2..4), decode_waves (0 = one per resident slot, or the
+    persistent decode grid size)."""
+    old = get_tuning()
+    new = dict(old)
+    for name, value in overrides.items():
+        if name not in new:
+            raise TypeError(f"unknown tuning field {name!r}")
+        new[name] = int(value)
+    check(lib().pf_set_tuning(ctypes.byref(Tuning(**new))), "pf_set_tuning")
+    try:
+        yield new
+    finally:
+        check(lib().pf_set_tuning(ctypes.byref(Tuning(**old))), "pf_set_tuning")

@@ -12,8 +12,14 @@ training users to apply RoPE outside, README.md:156-157): when q, k or v
 requires grad, the forward rotates q and k once (pf_rope), runs the
 LSE-saving forward on the rotated tensors and saves them; the backward runs
 the standard backward (pf_attn_bwd) and maps dq, dk back through the
-transpose rotation x*cos - rotate_half(x)*sin (pf_rope, inverse) -- RoPE is
-an orthogonal map per position, so its VJP is its inverse.
+transpose of the rotation (pf_rope, inverse): g*cos + rotate_half^T(g*sin),
+rotate_half^T([y1, y2]) = [y2, -y1]. That is the VJP for any table, also one
+whose halves differ (for precompute_rope's tables it equals the inverse
+rotation).
+
+Numerics: the rotated Q and K are rounded once to the input dtype before the
+bf16/f16 MFMA (the reference keeps them in float32 and runs a float32 dot,
+fused_rope.py:75-78); float32 inputs keep float32 throughout.
 """
 
 from __future__ import annotations
