@@ -11,15 +11,17 @@
  * Conventions
  *  - Layout: every tensor is dense row-major (C-contiguous) in the shape given
  *    in the struct comments; element strides are implied by the shape.
- *  - Ownership: the caller allocates every buffer, including workspaces.
- *    Entry points never allocate, free or synchronise; they enqueue kernels on
- *    `stream` and return.
+ *  - Ownership: the caller allocates every buffer, including workspaces
+ *    (pf_paged_attn_noalloc instead uses a static device array of the
+ *    library's). Entry points never allocate, free or synchronise; they
+ *    enqueue kernels on `stream` and return.
  *  - Validation happens on the host before any HIP call; a rejected call
  *    enqueues nothing. After enqueueing, hipGetLastError() is checked and a
  *    launch failure is reported as PF_ERR_LAUNCH.
  *  - Thread safety: reentrant. The only state is the process-wide tuning
- *    (pf_set_tuning) and a per-device cache of the CU count and kernel
- *    occupancy, filled once per device under std::call_once.
+ *    (pf_set_tuning), a per-device cache of the CU count and kernel
+ *    occupancy (filled once per device under std::call_once) and the
+ *    per-device scratch array of pf_paged_attn_noalloc (see there).
  *  - Data types: dtype tags PF_DTYPE_F32 / PF_DTYPE_BF16 / PF_DTYPE_F16 name
  *    the storage type of q/k/v/o (and do/dq/dk/dv); all arithmetic is float32
  *    (MFMA with float32 accumulation). LSE / delta are always float32.
@@ -233,6 +235,31 @@ typedef struct {
 
 size_t pf_paged_attn_workspace_size(const pf_paged_attn_args* args);
 int pf_paged_attn(const pf_paged_attn_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged single-query attention that allocates nothing and takes no
+ * workspace. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc. Same arguments, kernels and results
+ * as pf_paged_attn (bit for bit); `workspace` / `workspace_bytes` are
+ * ignored. The split-KV partials go to a static device array of
+ * PF_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
+ * process ends.
+ *  - A call whose partials need more than PF_NOALLOC_SCRATCH_BYTES
+ *    (pf_paged_attn_workspace_size(args) larger) returns PF_ERR_WORKSPACE
+ *    and enqueues nothing. bf16/f16, head_dim 128, page_size % 4 == 0 (the
+ *    streaming kernel) needs at most about 16.3 MiB at the default tuning on
+ *    a 256-CU device, whatever the batch; the generic kernel needs about
+ *    batch * num_heads * splits * 520 bytes.
+ *  - Every call on one GPU shares that GPU's array: calls that overlap on
+ *    one GPU (different streams, or other host threads) race on it and must
+ *    be serialised by the caller. Nothing carries over between calls.
+ *  - The array's device address is resolved once per device
+ *    (hipGetSymbolAddress) at the first call on it; no call allocates or
+ *    frees.
+ * ------------------------------------------------------------------------- */
+#define PF_NOALLOC_SCRATCH_BYTES (32u << 20)
+int pf_paged_attn_noalloc(const pf_paged_attn_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * KV-cache writes on device. Replaces the decode loop's `_cache_write`

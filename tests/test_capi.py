@@ -290,3 +290,20 @@ def test_tuning_round_trip_and_rejections(L):
     with pytest.raises(TypeError):
         with _lib.tuning(block_q=64):
             pass
+
+
+def test_paged_noalloc_refuses_on_host(L):
+    """pf_paged_attn_noalloc validates like pf_paged_attn and refuses, before
+    any HIP call, a problem whose partials exceed its static array."""
+    text = open(HEADER).read()
+    m = re.search(r"#define PF_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    scratch = int(m.group(1)) << int(m.group(2))
+    bad = _lib.PagedArgs(q=8, k_pages=8, v_pages=8, block_tables=8, context_lens=8, o=8, batch=2,
+                         num_heads=3, num_kv_heads=2, num_pages=4, page_size=5, head_dim=128,
+                         pages_per_seq=2, sm_scale=0.1, dtype=0, workspace=None, workspace_bytes=0)
+    assert L.pf_paged_attn_noalloc(bad, None) == _lib.PF_ERR_INVALID  # 3 % 2 heads
+    big = _lib.PagedArgs(q=8, k_pages=8, v_pages=8, block_tables=8, context_lens=8, o=8, batch=4096,
+                         num_heads=32, num_kv_heads=8, num_pages=8, page_size=5, head_dim=128,
+                         pages_per_seq=2, sm_scale=0.1, dtype=0, workspace=None, workspace_bytes=0)
+    assert L.pf_paged_attn_workspace_size(big) > scratch
+    assert L.pf_paged_attn_noalloc(big, None) == _lib.PF_ERR_WORKSPACE

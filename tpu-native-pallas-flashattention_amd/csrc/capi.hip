@@ -420,6 +420,66 @@ int pf_paged_attn(const pf_paged_attn_args* a, void* stream) {
   return finish(pf::launch_decode(p, a->dtype, true, (hipStream_t)stream));
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Paged decode with no caller workspace (pf_paged_attn_noalloc): the split-KV
+// partials live in `scratch`, a file-scope device array that every GPU holds
+// once, for the life of the process. On the host `scratch` names a host-side
+// stand-in, not device memory: its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) and only that
+// address is handed to the kernels. Every call on one GPU shares the array;
+// nothing in it needs clearing between calls (each launch writes every
+// partial slot its combine step reads), and calls that overlap on one GPU
+// (concurrent streams) race on it.
+// ---------------------------------------------------------------------------
+namespace {
+
+static_assert(PF_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch keeps the workspace alignment");
+static __device__ __align__(256) char scratch[PF_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+
+struct ScratchAddr {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipErrorNotInitialized;
+};
+ScratchAddr g_scratch[kMaxScratchDevices];
+
+// Device address of the current device's `scratch` (PF_OK), resolved on the
+// first call on each device.
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return PF_ERR_LAUNCH;
+  ScratchAddr& s = g_scratch[dev];
+  std::call_once(s.once, [&s] { s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch)); });
+  if (s.err != hipSuccess || s.ptr == nullptr) return PF_ERR_LAUNCH;
+  *out = s.ptr;
+  return PF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pf_paged_attn_noalloc(const pf_paged_attn_args* a, void* stream) {
+  pf::DecodeParams p;
+  int st = fill_paged(a, &p);
+  if (st != PF_OK) return st;
+  if (!a->q || !a->k_pages || !a->v_pages || !a->o || !a->context_lens) return PF_ERR_INVALID;
+  if (a->pages_per_seq > 0 && !a->block_tables) return PF_ERR_INVALID;
+  if (a->batch == 0) return PF_OK;
+  const size_t need = decode_ws_bytes(p);
+  if (need > (size_t)PF_NOALLOC_SCRATCH_BYTES) return PF_ERR_WORKSPACE;
+  void* ws = nullptr;
+  st = scratch_address(&ws);
+  if (st != PF_OK) return st;
+  st = bind_workspace(&p, ws, PF_NOALLOC_SCRATCH_BYTES);
+  if (st != PF_OK) return st;
+  return finish(pf::launch_decode(p, a->dtype, true, (hipStream_t)stream));
+}
+
 int pf_rope(const pf_rope_args* a, void* stream) {
   if (!a) return PF_ERR_INVALID;
   if (a->batch < 0 || a->heads < 0 || a->seq_len < 0 || a->head_dim < 2 || a->head_dim % 2 != 0)

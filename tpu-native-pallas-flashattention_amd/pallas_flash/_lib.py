@@ -131,6 +131,7 @@ SIGNATURES = {
     "pf_attn_decode": ([ctypes.POINTER(DecodeArgs), c_ptr], ctypes.c_int),
     "pf_paged_attn_workspace_size": ([ctypes.POINTER(PagedArgs)], ctypes.c_size_t),
     "pf_paged_attn": ([ctypes.POINTER(PagedArgs), c_ptr], ctypes.c_int),
+    "pf_paged_attn_noalloc": ([ctypes.POINTER(PagedArgs), c_ptr], ctypes.c_int),
     "pf_rope": ([ctypes.POINTER(RopeArgs), c_ptr], ctypes.c_int),
     "pf_kv_cache_write": ([ctypes.POINTER(KvWriteArgs), c_ptr], ctypes.c_int),
     "pf_paged_cache_write": ([ctypes.POINTER(PagedWriteArgs), c_ptr], ctypes.c_int),
