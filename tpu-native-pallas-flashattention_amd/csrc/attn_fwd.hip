@@ -9,8 +9,8 @@
 // query block); each wave owns 32 query rows of one head. A workgroup packs
 // hpw query heads of one GQA group (4 when the group size allows) x 128/hpw
 // rows, so the K/V tiles it stages serve all those heads. The grid is 1-D: heavy (late) query
-// blocks first for causal load balance, and the head groups sharing a KV
-// head on one XCD so they share K/V in that XCD's L2 (see xcd_remap).
+// blocks first for causal load balance, and the workgroups sharing a KV head
+// on one XCD so they share K/V in that XCD's L2 (fwd_work_item).
 //
 // Per 64-key block the workgroup stages K and V in LDS, double-buffered: the
 // global loads for block j+1 are in flight while block j is computed, and one
@@ -64,8 +64,20 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   constexpr int PF = 32 / MF::kK;    // P fragments per lane per block
   static_assert(BN == 64, "one K/V block is one 64-row tile");
 
-  // two buffers x (K tile, V tile)
-  __shared__ __attribute__((aligned(16))) char smem[4 * G::BYTES];
+  // Fused RoPE, 16-bit, all four waves on the same 32 query rows (hpw = 4):
+  // the workgroup's slice of the cos/sin tables (32 rows each, float32) is
+  // staged in LDS by one coalesced DMA and each lane reads its row from
+  // there. Loaded straight from global memory instead, every lane reads 512
+  // contiguous bytes of its own row, so each load instruction touches 64
+  // rows; those scattered loads, repeated by all four waves, were most of
+  // the fused forward's extra time. The slice occupies V buffer 1 (not
+  // loaded before the first block's barrier) and one more tile.
+  constexpr bool kStageTab = ROPE && ES == 2;
+  constexpr int kTabRows = 32;
+  constexpr int kTabBytes = kTabRows * D * 4;  // one table's slice
+  static_assert(!kStageTab || 2 * kTabBytes == 2 * G::BYTES, "table slices fill V buffer 1 + one tile");
+  // two buffers x (K tile, V tile) [+ the table tile]
+  __shared__ __attribute__((aligned(16))) char smem[(kStageTab ? 5 : 4) * G::BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,16 +85,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const int hh = lane >> 5;
   const int l32 = lane & 31;
 
-  // work item = (query block, batch, kv head, head group); the workgroup's
+  // work item = (batch, kv head, head group, query block); the workgroup's
   // waves split into hpw heads x (4 / hpw) 32-row slices.
-  const int n_hg = p.g / p.hpw;
-  const int w = xcd_remap(blockIdx.x, p.n_work, n_hg);
-  const int hg = w % n_hg;
-  int rest = w / n_hg;
-  const int kvh = rest % p.Hkv;
-  rest /= p.Hkv;
-  const int b = rest % p.B;
-  const int qblk = p.n_qblk - 1 - rest / p.B;
+  int b, kvh, hg, qblk;
+  fwd_work_item(blockIdx.x, p, b, kvh, hg, qblk);
   const int wph = 4 / p.hpw;  // waves per head
   const int h = kvh * p.g + hg * p.hpw + wv / wph;
 
@@ -97,8 +103,6 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   // ---- staging: K/V rows at or past kv_len lie outside the buffer resources
   // and load as zeros (never read from memory). K and V go global -> LDS by
   // DMA (with fused RoPE, p.k is the K rotated once by pf_rope_rotate_k_kernel).
-  // The first tiles are requested before Q is loaded (and, with RoPE,
-  // rotated), so the two memory latencies overlap.
   const uint32_t kv_bytes = (uint32_t)p.kv_len * (uint32_t)(D * ES);
   const i32x4 krs = make_desc(Kb, kv_bytes);
   const i32x4 vrs = make_desc(Vb, kv_bytes);
@@ -108,41 +112,114 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   if constexpr (CAUSAL) kv_end = min(kv_end, min(q0 + p.rpw, p.Sq));
   const int nblk = (kv_end + BN - 1) / BN;
   // LDS: K tiles at [0, 2 BYTES) (block j in j & 1), V tiles after them.
-  if (nblk > 0) {
-    dma.load(krs, 0, smem);
-    dma.load(vrs, 0, smem + 2 * G::BYTES);
-    if (nblk > 1) dma.load(krs, BN, smem + G::BYTES);
-  }
+  auto first_tiles = [&]() {
+    if (nblk > 0) {
+      dma.load(krs, 0, smem);
+      dma.load(vrs, 0, smem + 2 * G::BYTES);
+      if (nblk > 1) dma.load(krs, BN, smem + G::BYTES);
+    }
+  };
+  // Without RoPE the first tiles are requested before Q, which only the
+  // first block's MFMAs (after those tiles) need. With RoPE, Q and its table
+  // rows go first: vmcnt counts loads in issue order, so the rotation would
+  // otherwise wait for the tiles too.
+  if constexpr (!ROPE) first_tiles();
 
   // ---- Q fragment (B operand of S^T): lane holds Q[qrow][hh*HALF, +HALF).
-  Frag qf[QF];
+  // Rows past Sq load row 0 (in bounds; no branch around the loads) and are
+  // zeroed after the wait.
+  const bool qvalid = qrow < p.Sq;
+  const bool stage_tab = kStageTab && p.hpw == 4;  // workgroup-uniform
+  char* const tab = smem + 3 * G::BYTES;            // cos slice, then sin slice
+  u32x4 qc[HALF / EPC];
+  [[maybe_unused]] f32x4 ct[ROPE ? HALF / 4 : 1], st[ROPE ? HALF / 4 : 1];
   {
-    u32x4 qc[HALF / EPC];
-    if (qrow < p.Sq) {
-      const T* qr = Qb + (int64_t)qrow * D;
-      if constexpr (ROPE) {
-        const float* cs = p.q_cos + (int64_t)qrow * D;
-        const float* sn = p.q_sin + (int64_t)qrow * D;
-        const float sgn = hh ? 1.f : -1.f;
+    const T* qr = Qb + (int64_t)(qvalid ? qrow : 0) * D + hh * HALF;
 #pragma unroll
-        for (int c = 0; c < HALF / EPC; ++c) {
-          float x[EPC], xp[EPC], y[EPC];
-          chunk_to_f32<T>(ldg16(qr + hh * HALF + c * EPC), x);
-          chunk_to_f32<T>(ldg16(qr + (1 - hh) * HALF + c * EPC), xp);
+    for (int c = 0; c < HALF / EPC; ++c) qc[c] = ldg16(qr + c * EPC);
+    if constexpr (ROPE) {
+      if (stage_tab) {
+        // Table row q0 + r lands at tab + r * 4D with its 16-byte chunk ch at
+        // position ch ^ (r & 15): the 16 lanes of an LDS read (16 rows, one
+        // chunk index) then hit 16 different bank groups. Rows past Sq lie
+        // outside the descriptors and arrive as zeros.
+        constexpr int CPRT = D / 4;  // 16-byte chunks per table row
+        constexpr int PER = kTabRows * CPRT / 256;
+        const uint32_t nb = (uint32_t)max(0, min(kTabRows, p.Sq - q0)) * (uint32_t)(D * 4);
+        const i32x4 cd = make_desc(p.q_cos + (int64_t)q0 * D, nb);
+        const i32x4 sd = make_desc(p.q_sin + (int64_t)q0 * D, nb);
+        const int w = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
-          for (int e = 0; e < EPC; ++e) {
-            const int d = hh * HALF + c * EPC + e;
-            y[e] = x[e] * cs[d] + sgn * xp[e] * sn[d];
-          }
-          qc[c] = f32_to_chunk<T>(y);
+        for (int u = 0; u < PER; ++u) {
+          const int slot = 64 * (4 * u + w) + lane;  // 16-byte slot within a slice
+          const int r = slot / CPRT, pos = slot % CPRT;
+          const uint32_t voff = (uint32_t)(r * D * 4 + 16 * (pos ^ (r & 15)));
+          const uint32_t la = __builtin_amdgcn_readfirstlane(lds_u32(tab) + 16 * 64 * (4 * u + w));
+          dma16(cd, voff, la);
+          dma16(sd, voff, la + kTabBytes);
         }
       } else {
+        const float* cr = p.q_cos + (int64_t)(qvalid ? qrow : 0) * D + hh * HALF;
+        const float* sr = p.q_sin + (int64_t)(qvalid ? qrow : 0) * D + hh * HALF;
 #pragma unroll
-        for (int c = 0; c < HALF / EPC; ++c) qc[c] = ldg16(qr + hh * HALF + c * EPC);
+        for (int c = 0; c < HALF / 4; ++c) {
+          ct[c] = *reinterpret_cast<const f32x4*>(cr + 4 * c);
+          st[c] = *reinterpret_cast<const f32x4*>(sr + 4 * c);
+        }
       }
-    } else {
+    }
+  }
+
+  if constexpr (ROPE) first_tiles();
+
+  Frag qf[QF];
+  {
+    if (!qvalid) {
 #pragma unroll
       for (int c = 0; c < HALF / EPC; ++c) qc[c] = (u32x4){0u, 0u, 0u, 0u};
+    }
+    if constexpr (ROPE) {
+      if (stage_tab) {
+        // The table DMA went out before the K/V tiles' (3 tiles of
+        // TileDma::PER_T loads per lane at most): wait for it alone, then for
+        // every wave's part of it.
+        constexpr int KV_LOADS = TileDma<T, D>::PER_T;
+        if (nblk > 1) wait_vm<3 * KV_LOADS>();
+        else wait_vm<2 * KV_LOADS>();
+        __syncthreads();
+        const int r = l32;  // the lane's row within the slice (wq0 == q0 here)
+#pragma unroll
+        for (int c = 0; c < HALF / 4; ++c) {
+          const int ch = hh * (HALF / 4) + c;
+          const char* a = tab + r * D * 4 + 16 * (ch ^ (r & 15));
+          ct[c] = __builtin_bit_cast(f32x4, lds16(a));
+          st[c] = __builtin_bit_cast(f32x4, lds16(a + kTabBytes));
+        }
+      }
+      // x*cos + rotate_half(x)*sin in float32 (fused_rope.py:43-50, :75-78):
+      // element d of half hh is x[d] cos[d] - x[d + HALF] sin[d] (hh = 0) or
+      // x[d] cos[d] + x[d - HALF] sin[d] (hh = 1); the partner half lives in
+      // lane l ^ 32 and is exchanged with v_permlane32_swap (which returns
+      // the pair's two values; partner = both ^ own, whatever their order).
+      const float sgn = hh ? 1.f : -1.f;
+#pragma unroll
+      for (int c = 0; c < HALF / EPC; ++c) {
+        u32x4 pc;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const auto r = __builtin_amdgcn_permlane32_swap(qc[c][w], qc[c][w], false, false);
+          pc[w] = r[0] ^ r[1] ^ qc[c][w];
+        }
+        float x[EPC], xp[EPC], y[EPC];
+        chunk_to_f32<T>(qc[c], x);
+        chunk_to_f32<T>(pc, xp);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const int i = c * EPC + e;  // element within the half
+          y[e] = x[e] * ct[i / 4][i % 4] + sgn * xp[e] * st[i / 4][i % 4];
+        }
+        qc[c] = f32_to_chunk<T>(y);
+      }
     }
     // A negative scale is applied as |scale| on -Q (exact sign flips), so the
     // softmax below only ever sees a non-negative scale.
@@ -403,50 +480,76 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   }
 }
 
-// Row rotation: the K prologue of the fused-RoPE forward and pf_rope. Each
-// thread rotates one 16-byte chunk of the first half of a row together with
-// its partner chunk D/2 further, then rounds once to T. Row `pos` of each
-// (b, h) uses table row `pos`; rows at or past kv_len are not touched (the
-// attention kernel never reads them). With halves x1 = x[:D/2], x2 = x[D/2:]
-// and table halves c1, c2, s1, s2 of row pos:
+// Row rotation: the K prologue of the fused-RoPE forward and pf_rope. A
+// thread owns one 16-byte chunk of the first half of a row position `pos`
+// together with its partner chunk D/2 further, loads that position's table
+// values once and applies them to the same chunks of kHeadsPerThread rows
+// (one per (batch, head), all at `pos`), rounding once to T. Rows at or past
+// kv_len are not touched (the attention kernel never reads them). With halves
+// x1 = x[:D/2], x2 = x[D/2:] and table halves c1, c2, s1, s2 of row pos:
 //   forward (fused_rope.py:43-50, :75-78: x*cos + rotate_half(x)*sin)
 //     y1 = x1 c1 - x2 s1,  y2 = x2 c2 + x1 s2;
 //   inverse = the transpose of that linear map (the VJP of the forward one,
 //   exact for any table, also when the halves of a table row differ)
 //     y1 = x1 c1 + x2 s2,  y2 = x2 c2 - x1 s1.
+// Consecutive threads take consecutive chunks, then positions, so each
+// (batch, head)'s rows are read and written contiguously.
+constexpr int kHeadsPerThread = 4;
+
 template <typename T, int D, bool INVERSE>
 __global__ __launch_bounds__(256) void pf_rope_rotate_k_kernel(const T* __restrict__ k, T* __restrict__ out,
                                                                const float* __restrict__ cosb,
                                                                const float* __restrict__ sinb, int Sk,
-                                                               int kv_len, int64_t n_items) {
+                                                               int kv_len, int n_bh, int64_t n_items) {
   constexpr int EPC = 16 / (int)sizeof(T);
   constexpr int HC = D / 2 / EPC;  // chunks per half row
   const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (item >= n_items) return;
   const int pc = (int)(item % HC);
-  const int64_t rr = item / HC;           // row over (batch, kv head, position < kv_len)
+  const int64_t rr = item / HC;  // (head group, position < kv_len)
   const int pos = (int)(rr % kv_len);
-  const int64_t bh = rr / kv_len;
-  const int64_t row = bh * Sk + pos;
-  const T* src = k + row * D + pc * EPC;
-  float a[EPC], bb[EPC], ra[EPC], rb[EPC];
-  chunk_to_f32<T>(ldg16(src), a);
-  chunk_to_f32<T>(ldg16(src + D / 2), bb);
+  const int bh0 = (int)(rr / kv_len) * kHeadsPerThread;
+  const int nh = min(kHeadsPerThread, n_bh - bh0);
   const float* cs = cosb + (int64_t)pos * D + pc * EPC;
   const float* sn = sinb + (int64_t)pos * D + pc * EPC;
+  float c1[EPC], c2[EPC], s1[EPC], s2[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) {
-    if constexpr (INVERSE) {
-      ra[e] = a[e] * cs[e] + bb[e] * sn[D / 2 + e];
-      rb[e] = bb[e] * cs[D / 2 + e] - a[e] * sn[e];
-    } else {
-      ra[e] = a[e] * cs[e] - bb[e] * sn[e];
-      rb[e] = bb[e] * cs[D / 2 + e] + a[e] * sn[D / 2 + e];
+    c1[e] = cs[e];
+    c2[e] = cs[D / 2 + e];
+    s1[e] = sn[e];
+    s2[e] = sn[D / 2 + e];
+  }
+  u32x4 lo[kHeadsPerThread], hi[kHeadsPerThread];
+#pragma unroll
+  for (int j = 0; j < kHeadsPerThread; ++j) {
+    if (j < nh) {
+      const T* src = k + ((int64_t)(bh0 + j) * Sk + pos) * D + pc * EPC;
+      lo[j] = ldg16(src);
+      hi[j] = ldg16(src + D / 2);
     }
   }
-  T* dst = out + row * D + pc * EPC;
-  stg16(dst, f32_to_chunk<T>(ra));
-  stg16(dst + D / 2, f32_to_chunk<T>(rb));
+#pragma unroll
+  for (int j = 0; j < kHeadsPerThread; ++j) {
+    if (j < nh) {
+      float a[EPC], bb[EPC], ra[EPC], rb[EPC];
+      chunk_to_f32<T>(lo[j], a);
+      chunk_to_f32<T>(hi[j], bb);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        if constexpr (INVERSE) {
+          ra[e] = a[e] * c1[e] + bb[e] * s2[e];
+          rb[e] = bb[e] * c2[e] - a[e] * s1[e];
+        } else {
+          ra[e] = a[e] * c1[e] - bb[e] * s1[e];
+          rb[e] = bb[e] * c2[e] + a[e] * s2[e];
+        }
+      }
+      T* dst = out + ((int64_t)(bh0 + j) * Sk + pos) * D + pc * EPC;
+      stg16(dst, f32_to_chunk<T>(ra));
+      stg16(dst + D / 2, f32_to_chunk<T>(rb));
+    }
+  }
 }
 
 template <typename T, int D>
@@ -473,15 +576,16 @@ template <typename T, int D>
 hipError_t rotate_typed(const void* k, void* out, const float* cs, const float* sn, int B, int Hkv, int Sk,
                         int kv_len, bool inverse, hipStream_t st) {
   constexpr int HC = D / 2 / (16 / (int)sizeof(T));
-  const int64_t n_items = (int64_t)B * Hkv * kv_len * HC;
+  const int n_bh = B * Hkv;
+  const int64_t n_items = (int64_t)((n_bh + kHeadsPerThread - 1) / kHeadsPerThread) * kv_len * HC;
   if (n_items == 0) return hipSuccess;
   const dim3 grid((unsigned)((n_items + 255) / 256)), block(256);
   if (inverse)
     hipLaunchKernelGGL((pf_rope_rotate_k_kernel<T, D, true>), grid, block, 0, st, static_cast<const T*>(k),
-                       static_cast<T*>(out), cs, sn, Sk, kv_len, n_items);
+                       static_cast<T*>(out), cs, sn, Sk, kv_len, n_bh, n_items);
   else
     hipLaunchKernelGGL((pf_rope_rotate_k_kernel<T, D, false>), grid, block, 0, st, static_cast<const T*>(k),
-                       static_cast<T*>(out), cs, sn, Sk, kv_len, n_items);
+                       static_cast<T*>(out), cs, sn, Sk, kv_len, n_bh, n_items);
   return hipGetLastError();
 }
 

@@ -152,14 +152,8 @@ __global__ __launch_bounds__(256, 1) void pf_attn_fwd_w64_kernel(FwdParams p) {
 
   // work item = (query block, batch, kv head, head group); the waves split
   // into hpw heads x (4 / hpw) 64-row slices.
-  const int n_hg = p.g / p.hpw;
-  const int w = xcd_remap(blockIdx.x, p.n_work, n_hg);
-  const int hg = w % n_hg;
-  int rest = w / n_hg;
-  const int kvh = rest % p.Hkv;
-  rest /= p.Hkv;
-  const int b = rest % p.B;
-  const int qblk = p.n_qblk - 1 - rest / p.B;
+  int b, kvh, hg, qblk;
+  fwd_work_item(blockIdx.x, p, b, kvh, hg, qblk);
   const int wph = 4 / p.hpw;
   const int h = kvh * p.g + hg * p.hpw + wv / wph;
   const int q0 = qblk * p.rpw;

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "pf_common.hpp"
+
 namespace pf {
 
 // Forward prefill (optionally with fused RoPE).
@@ -25,6 +27,23 @@ struct FwdParams {
   int n_qblk;        // ceil(Sq / rpw)
   int n_work;        // B * Hq / hpw * n_qblk
 };
+
+// Work item of forward workgroup `bid`: (batch b, kv head kvh, head group hg
+// of the GQA group, query block qblk). Items run in (query block, batch, kv
+// head, head group) order, heavy (late, causal) query blocks first, with the
+// head groups of one kv head on one XCD (xcd_remap: workgroups are
+// dispatched round-robin over the 8 XCDs, each with its own L2). A bijection
+// of [0, n_work).
+__device__ inline void fwd_work_item(int bid, const FwdParams& p, int& b, int& kvh, int& hg, int& qblk) {
+  const int n_hg = p.g / p.hpw;
+  const int w = xcd_remap(bid, p.n_work, n_hg);
+  hg = w % n_hg;
+  int rest = w / n_hg;
+  kvh = rest % p.Hkv;
+  rest /= p.Hkv;
+  b = rest % p.B;
+  qblk = p.n_qblk - 1 - rest / p.B;
+}
 
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream);
