@@ -161,9 +161,11 @@ def _check_step(dt, q, kn, vn, kc0, vc0, kc, vc, o, pos, cos, sin, ring):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("Hq,Hkv", [(8, 2), (32, 8), (4, 4)])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 2), (32, 8), (4, 4), (32, 1), (24, 1)])
 @pytest.mark.parametrize("ring", [False, True])
 def test_decode_step_matches_oracle(dt, Hq, Hkv, ring):
+    """(32, 1) and (24, 1): the group spans two 16-head slices, each of which
+    streams (and patches) the new token's stage; only slice 0 writes the cache."""
     note(f"decode_step dt={dt} Hq={Hq} Hkv={Hkv} ring={ring}")
     rng = np.random.default_rng(15)
     B, C, D = 4, 200, 128

@@ -527,10 +527,10 @@ int pf_paged_cache_write(const pf_paged_cache_write_args* a, void* stream) {
   return finish(pf::launch_paged_cache_write(p, a->dtype, a->head_dim, (hipStream_t)stream));
 }
 
-// Workspace of the decode step: rotated queries, per-batch live lengths, then
-// the streaming decode's partials.
-static int fill_decode_step(const pf_attn_decode_step_args* a, pf::DecodeParams* p, size_t* q_bytes,
-                            size_t* len_bytes) {
+// The fused decode step is one streaming-decode launch in its step mode
+// (decode_stream.hip, PG == 1) plus the combine; its workspace is the split
+// partials only.
+static int fill_decode_step(const pf_attn_decode_step_args* a, pf::DecodeParams* p) {
   if (!a) return PF_ERR_INVALID;
   if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->cache_size < 1) return PF_ERR_INVALID;
   if (a->num_heads % a->num_kv_heads != 0) return PF_ERR_INVALID;
@@ -543,6 +543,7 @@ static int fill_decode_step(const pf_attn_decode_step_args* a, pf::DecodeParams*
   if (!pf::decode_stream_supported(a->dtype, a->head_dim, false, 0)) return PF_ERR_UNSUPPORTED;
   if ((int64_t)a->cache_size * a->head_dim * 2 >= ((int64_t)1 << 31)) return PF_ERR_UNSUPPORTED;
   *p = pf::DecodeParams{};
+  p->q = a->q;
   p->k = a->k_cache;
   p->v = a->v_cache;
   p->o = a->o;
@@ -553,43 +554,36 @@ static int fill_decode_step(const pf_attn_decode_step_args* a, pf::DecodeParams*
   p->cache_size = a->cache_size;
   p->cache_len = a->cache_size;
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p->positions = a->positions;
+  p->pos_stride = a->positions_stride;
+  p->ring = a->ring;
+  p->rope_cos = a->cos;
+  p->rope_sin = a->sin;
+  p->rope_len = a->rope_len;
+  p->k_new = a->k_new;
+  p->v_new = a->v_new;
+  p->k_out = a->k_cache;
+  p->v_out = a->v_cache;
   if (stream_setup(p, a->num_heads / a->num_kv_heads) <= 0) return PF_ERR_LAUNCH;
-  *q_bytes = align256((size_t)a->batch * a->num_heads * a->head_dim * 2);
-  *len_bytes = align256((size_t)a->batch * sizeof(int32_t));
   return PF_OK;
 }
 
 size_t pf_attn_decode_step_workspace_size(const pf_attn_decode_step_args* a) {
   pf::DecodeParams p;
-  size_t qb = 0, lb = 0;
-  if (fill_decode_step(a, &p, &qb, &lb) != PF_OK) return 0;
-  return qb + lb + decode_ws_bytes(p);
+  if (fill_decode_step(a, &p) != PF_OK) return 0;
+  return decode_ws_bytes(p);
 }
 
 int pf_attn_decode_step(const pf_attn_decode_step_args* a, void* stream) {
   pf::DecodeParams p;
-  size_t qb = 0, lb = 0;
-  int st = fill_decode_step(a, &p, &qb, &lb);
+  int st = fill_decode_step(a, &p);
   if (st != PF_OK) return st;
   if (a->batch == 0) return PF_OK;
   if (!a->q || !a->k_new || !a->v_new || !a->k_cache || !a->v_cache || !a->o || !a->positions)
     return PF_ERR_INVALID;
-  const size_t need = qb + lb + decode_ws_bytes(p);
-  if (!a->workspace || a->workspace_bytes < need || ((uintptr_t)a->workspace & 255) != 0)
-    return PF_ERR_WORKSPACE;
-  char* ws = static_cast<char*>(a->workspace);
-  pf::DecodeStepParams sp{a->q, a->k_new, a->v_new, a->k_cache, a->v_cache, ws,
-                          reinterpret_cast<int32_t*>(ws + qb), a->positions, a->positions_stride,
-                          a->cos, a->sin, a->rope_len, a->batch, a->num_heads, a->num_kv_heads,
-                          a->cache_size, a->ring};
-  st = bind_workspace(&p, ws + qb + lb, a->workspace_bytes - qb - lb);
+  st = bind_workspace(&p, a->workspace, a->workspace_bytes);
   if (st != PF_OK) return st;
-  p.q = ws;                                            // rotated queries
-  p.context_lens = reinterpret_cast<int32_t*>(ws + qb);  // device-side live lengths
-  const hipStream_t s = (hipStream_t)stream;
-  st = finish(pf::launch_decode_step_prep(sp, a->dtype, a->head_dim, s));
-  if (st != PF_OK) return st;
-  return finish(pf::launch_decode(p, a->dtype, false, s));
+  return finish(pf::launch_decode(p, a->dtype, false, (hipStream_t)stream));
 }
 
 }  // extern "C"

@@ -106,20 +106,38 @@ struct Mfma16<f16_t> {
   }
 };
 
-// Clamp of a device-side length: contiguous cache (PG == 1) to its capacity,
-// paged pool to the table's reach.
-template <int PG>
-__device__ inline int clamp_len(const DecodeParams& p, int raw) {
-  return min(max(raw, 0), PG == 1 ? p.cache_size : p.pages_per_seq * p.page_size);
+// Live keys of a decode step whose new token is at `pos` (0 for an invalid
+// position: it attends nothing and writes nothing): linear cache pos + 1,
+// ring min(pos + 1, cache_size) (model.py:475-476).
+__device__ inline int step_len(const DecodeParams& p, int pos) {
+  const bool valid = pos >= 0 && (p.ring != 0 || pos < p.cache_size) &&
+                     (p.rope_cos == nullptr || pos < p.rope_len);
+  if (!valid) return 0;
+  return p.ring != 0 ? min(pos + 1, p.cache_size) : pos + 1;
 }
 
-// Valid keys of batch b.
+// Valid keys of batch b: PG == 0 the one cache_len; PG == 1 (decode step)
+// from b's position; paged: b's context length clamped to the table's reach.
+// len_lane reads per lane (b may differ across lanes), seq_len with scalar
+// loads (b wave-uniform).
+template <int PG>
+__device__ inline int len_lane(const DecodeParams& p, int b) {
+  if constexpr (PG == 0) {
+    return p.cache_len;
+  } else if constexpr (PG == 1) {
+    return step_len(p, p.positions[(int64_t)b * p.pos_stride]);
+  } else {
+    return min(max(p.context_lens[b], 0), p.pages_per_seq * p.page_size);
+  }
+}
 template <int PG>
 __device__ inline int seq_len(const DecodeParams& p, int b) {
-  if constexpr (PG != 0) {
-    return clamp_len<PG>(p, sload_i32(p.context_lens, b));
-  } else {
+  if constexpr (PG == 0) {
     return p.cache_len;
+  } else if constexpr (PG == 1) {
+    return step_len(p, sload_i32(p.positions, (int64_t)b * p.pos_stride));
+  } else {
+    return min(max(sload_i32(p.context_lens, b), 0), p.pages_per_seq * p.page_size);
   }
 }
 
@@ -171,7 +189,7 @@ __device__ inline int64_t locate(const DecodeParams& p, int J, int64_t s, Cursor
     int64_t base = 0;
     for (int b0 = 0; b0 < p.B; b0 += 64) {
       const int bb = b0 + lane;
-      const int Lb = bb < p.B ? clamp_len<PG>(p, p.context_lens[bb]) : 0;
+      const int Lb = bb < p.B ? len_lane<PG>(p, bb) : 0;
       const int64_t t = (int64_t)((Lb + kSK - 1) / kSK) * J;
       int64_t incl = t;  // inclusive scan over the 64 lanes
 #pragma unroll
@@ -196,11 +214,75 @@ __device__ inline int64_t locate(const DecodeParams& p, int J, int64_t s, Cursor
   }
 }
 
-// PG: 0 = contiguous cache, one length (cache_len) for every batch; 1 =
-// contiguous cache, per-batch lengths in device memory (context_lens, as the
-// fused decode step writes them); 32 = paged with page_size % 32 == 0 (one
-// page per stage); 4 = paged with page_size % 4 == 0 (one page per 4-row load).
+// With at most 64 batches one load of the per-batch lengths (a lane per
+// batch) gives everything both kernels need: lane bb's stage count T_bb =
+// ceil(L_bb / 32) * J, their inclusive scan `incl` and the total S. (More
+// batches take the looped scans of locate.)
+struct Lens64 {
+  int L;         // this lane's batch length (0 past B)
+  int64_t t;     // its stage count
+  int64_t incl;  // stage counts of batches <= this lane's, summed
+  int64_t tot;   // S, the total
+};
+template <int PG>
+__device__ inline Lens64 lens64(const DecodeParams& p, int J) {
+  const int lane = threadIdx.x & 63;
+  Lens64 r;
+  r.L = lane < p.B ? len_lane<PG>(p, lane) : 0;
+  r.t = (int64_t)((r.L + kSK - 1) / kSK) * J;
+  r.incl = r.t;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(r.incl, o);
+    if (lane >= o) r.incl += y;
+  }
+  r.tot = uni64(__shfl(r.incl, 63));
+  return r;
+}
+
+// The stages of wave w of W: their count (returned) and, if any, the cursor
+// of the first one.
+template <int PG>
+__device__ inline int64_t wave_plan(const DecodeParams& p, int J, int W, int w, Cursor* cc) {
+  if (PG != 0 && p.B <= 64) {
+    const Lens64 ls = lens64<PG>(p, J);
+    const int64_t s0 = wave_start(ls.tot, W, w);
+    const int64_t n = wave_start(ls.tot, W, w + 1) - s0;
+    if (n > 0) {
+      const uint64_t hit = __ballot(ls.incl > s0);
+      const int ln = __builtin_ctzll(hit);
+      const int64_t excl = __shfl(ls.incl - ls.t, ln);
+      const int Lh = __shfl(ls.L, ln);
+      const int nst = (Lh + kSK - 1) / kSK;
+      const int64_t r = s0 - excl;
+      *cc = Cursor{uni(ln), uni((int)(r / nst)), uni((int)(r % nst)), uni(nst), uni(Lh)};
+    }
+    return n;
+  }
+  const int64_t S = locate<PG>(p, J, -1, cc);
+  const int64_t s0 = wave_start(S, W, w);
+  const int64_t n = wave_start(S, W, w + 1) - s0;
+  if (n > 0) locate<PG>(p, J, s0, cc);
+  return n;
+}
+
+// PG: 0 = contiguous cache, one length (cache_len) for every batch; 1 = the
+// fused decode step (contiguous cache, per-batch positions in device memory,
+// see below); 32 = paged with page_size % 32 == 0 (one page per stage); 4 =
+// paged with page_size % 4 == 0 (one page per 4-row load).
 // QR: query rows staged per sequence (4 when the group has <= 4 heads, else 16).
+//
+// Decode step (PG == 1; model.py:340-347, :475-491): batch b's new token sits
+// at pos = positions[b * pos_stride], its slot is pos (ring: pos % C) and the
+// sequence is slots [0, step_len). At the start of each piece the wave reads
+// pos, rotates its query fragments with table row pos (rotate-half, float32,
+// rounded once to T: model.py:54-67) and prepares the new K row (rotated the
+// same way) and V row in registers. The stage holding the slot is patched in
+// LDS with those rows after its DMA lands -- the cache still holds the old
+// slot contents, and no other stage holds that row -- and the wave that owns
+// head slice 0 writes them to the cache slot. Every wave that reads the slot
+// (one per head slice) patches its own copy, so no wave depends on another's
+// global write within the launch.
 template <typename T, int PG, int NS, int QR>
 __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
   using MF = Mfma16<T>;
@@ -219,11 +301,8 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
   const int w = blockIdx.x;
 
   Cursor cc;
-  const int64_t S = locate<PG>(p, J, -1, &cc);
-  const int64_t s_begin = wave_start(S, W, w);
-  const int64_t n = wave_start(S, W, w + 1) - s_begin;  // stages of this wave
+  const int64_t n = wave_plan<PG>(p, J, W, w, &cc);  // stages of this wave
   if (n <= 0) return;
-  locate<PG>(p, J, s_begin, &cc);
 
   const uint32_t lds0 = lds_u32(smem);
   const T* Kb = static_cast<const T*>(p.k);
@@ -296,12 +375,101 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
     }
   };
 
+  // ---- decode step (PG == 1) --------------------------------------------
+  // Per piece: the token's position, this lane's chunk of the new K row
+  // (lanes 0-15, chunk i16, and its rotate-half partner i16 ^ 8) or V row
+  // (lanes 16-31), and the table values the lane's rotations use (K: elements
+  // 8 i16 .. +7; Q: 32 s + 8 h .. +7 for s = 0..3).
+  struct StepData {
+    int pos;
+    u32x4 kv, kvp;
+    f32x4 kc[2], ks[2];
+    f32x4 qc[4][2], qs[4][2];
+  };
+  [[maybe_unused]] auto step_load = [&](const Cursor& c, StepData& d) {
+    d.pos = sload_i32(p.positions, (int64_t)c.b * p.pos_stride);  // valid: the piece has keys
+    const int kvh = c.j / n_hc;
+    const int64_t src = ((int64_t)c.b * p.Hkv + kvh) * 128;
+    if (lane < 32) {
+      const T* nb = static_cast<const T*>(lane < 16 ? p.k_new : p.v_new) + src;
+      d.kv = ldg16(nb + 8 * i16);
+      d.kvp = ldg16(nb + 8 * (i16 ^ 8));
+    }
+    if (p.rope_cos != nullptr) {
+      const float* cr = p.rope_cos + (int64_t)d.pos * 128;
+      const float* sr = p.rope_sin + (int64_t)d.pos * 128;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        d.kc[u] = *reinterpret_cast<const f32x4*>(cr + 8 * i16 + 4 * u);
+        d.ks[u] = *reinterpret_cast<const f32x4*>(sr + 8 * i16 + 4 * u);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          d.qc[s4][u] = *reinterpret_cast<const f32x4*>(cr + 32 * s4 + 8 * h + 4 * u);
+          d.qs[s4][u] = *reinterpret_cast<const f32x4*>(sr + 32 * s4 + 8 * h + 4 * u);
+        }
+      }
+    }
+  };
+  // Rotate-half RoPE of 8 consecutive elements d0 .. d0 + 7 of a 128-element
+  // row whose partner elements (d +- 64) are in xp, with those elements'
+  // table values: y = x cos - x' sin (first half), x cos + x' sin (second
+  // half), float32, rounded once to T (model.py:54-67; fused_rope.py:43-50).
+  auto rope8 = [&](const u32x4& x, const u32x4& xp, const f32x4* c, const f32x4* sn, bool first_half) -> u32x4 {
+    float a[8], b2[8], y[8];
+    chunk_to_f32<T>(x, a);
+    chunk_to_f32<T>(xp, b2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float ce = c[e >> 2][e & 3], se = sn[e >> 2][e & 3];
+      y[e] = first_half ? a[e] * ce - b2[e] * se : a[e] * ce + b2[e] * se;
+    }
+    return f32_to_chunk<T>(y);
+  };
+  // New piece: the token's slot, the rotated query fragments (lane holds
+  // Q[head i16][32 s + 8 h + e]; the partner of s is s ^ 2) and this lane's
+  // new K (rotated) or V row chunk.
+  [[maybe_unused]] auto step_apply = [&](const StepData& d, Frag* q4, int& tslot, u32x4& row) {
+    tslot = p.ring != 0 ? d.pos % p.cache_size : d.pos;
+    row = d.kv;
+    if (p.rope_cos != nullptr) {
+      if (lane < 16) row = rope8(d.kv, d.kvp, d.kc, d.ks, i16 < 8);
+      u32x4 qx[4];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) qx[s4] = __builtin_bit_cast(u32x4, q4[s4]);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        q4[s4] = __builtin_bit_cast(Frag, rope8(qx[s4], qx[s4 ^ 2], d.qc[s4], d.qs[s4], s4 < 2));
+    }
+  };
+  // Stage holding the token's slot at row r: overwrite that row of the K and
+  // V tiles (after the stage's DMA landed), and write it to the cache once
+  // (head slice 0).
+  [[maybe_unused]] auto step_patch = [&](const Cursor& c, char* tK, char* tV, int r, int tslot, const u32x4& row) {
+    if (lane < 32) {
+      char* t = lane < 16 ? tK : tV;
+      sts16(t + r * kRowB + 16 * (i16 ^ sswz(r)), row);
+      const int kvh = c.j / n_hc, hc = c.j - kvh * n_hc;
+      if (hc == 0) {
+        T* out = static_cast<T*>(lane < 16 ? p.k_out : p.v_out);
+        stg16(out + (((int64_t)c.b * p.Hkv + kvh) * p.cache_size + tslot) * 128 + 8 * i16, row);
+      }
+    }
+    // this wave's LDS accesses run in order; keep the compiler from moving
+    // the tile reads above the stores
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  [[maybe_unused]] StepData pend;  // NS == 2: the step data of the piece the next stage opens
+
   // Prologue: the first NS - 1 stages.
   Cursor pc = cc;
 #pragma unroll
   for (int k = 0; k < NS - 1; ++k) {
     if (k < n) {
       issue(pc, k, k == 0 || pc.st == 0);
+      if constexpr (PG == 1 && NS == 2) step_load(pc, pend);  // stage 0 opens a piece
       cursor_next<PG>(pc, p, J);
     }
   }
@@ -333,12 +501,16 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
   float m_run = kNegInf, l_run = 0.f;
   int piece_st0 = 0;       // first stage (within the sequence) of the current piece
   bool first_piece = true;  // the current piece opens this wave's range
+  // Decode step: the current piece's token slot and its new K (lanes 0-15,
+  // 16-byte chunk i16) / V (lanes 16-31) row chunk.
+  [[maybe_unused]] int tok_slot = -1;
+  [[maybe_unused]] u32x4 new_row = (u32x4){0u, 0u, 0u, 0u};
 
   for (int64_t k = 0; k < n; ++k) {
     wait_stage<NS>(min((int64_t)(NS - 2), n - 1 - k));
     const int slot = (int)(k % NS);
-    const char* sK = smem + slot * kSlotB;
-    const char* sV = sK + kTileB;
+    char* const sK = smem + slot * kSlotB;
+    char* const sV = sK + kTileB;
     if (k == 0 || cc.st == 0) {
       // New piece: query fragments (B operand of S^T: lane holds
       // Q[head i16][d = 32 s + 8 h + 0..7]) and a fresh softmax state.
@@ -348,14 +520,32 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
         const u32x4 x = (i16 < QR) ? lds16(sQ + i16 * kRowB + 16 * ((4 * s + h) ^ i16)) : (u32x4){0u, 0u, 0u, 0u};
         qf[s] = __builtin_bit_cast(Frag, x);
       }
+      if constexpr (PG == 1) {
+        if constexpr (NS == 2) {
+          step_apply(pend, qf, tok_slot, new_row);  // loaded with the stage's DMA
+        } else {
+          StepData d;
+          step_load(cc, d);
+          step_apply(d, qf, tok_slot, new_row);
+        }
+      }
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) acc[dt] = (f32x4)(0.f);
       m_run = kNegInf;
       l_run = 0.f;
       piece_st0 = cc.st;
     }
+    if constexpr (PG == 1) {
+      // the stage holding the new token's slot: its row comes from registers
+      const int r = tok_slot - cc.st * kSK;
+      if (r >= 0 && r < kSK) step_patch(cc, sK, sV, r, tok_slot, new_row);
+    }
     if (k + NS - 1 < n) {
       issue(pc, (int)((k + NS - 1) % NS), pc.st == 0);
+      if constexpr (PG == 1 && NS == 2) {
+        // the next stage opens a piece: its step data arrive with its tiles
+        if (pc.st == 0) step_load(pc, pend);
+      }
       cursor_next<PG>(pc, p, J);
     }
 
@@ -456,23 +646,30 @@ __global__ __launch_bounds__(256) void pf_decode_stream_combine_kernel(DecodePar
   const int W = p.n_waves;
 
   // Global stage range [s0, s1) of this head's sequence.
-  Cursor dummy;
-  const int64_t S = locate<PG>(p, J, -1, &dummy);
-  int64_t before = 0;  // stages of batches < b
+  int64_t S, before = 0;  // all stages; stages of batches < b
   int L;
   if constexpr (PG == 0) {
+    Cursor dummy;
+    S = locate<PG>(p, J, -1, &dummy);
     L = p.cache_len;
     before = (int64_t)b * ((L + kSK - 1) / kSK) * J;
+  } else if (p.B <= 64) {
+    const Lens64 ls = lens64<PG>(p, J);
+    S = ls.tot;
+    before = uni64(__shfl(ls.incl - ls.t, b));
+    L = __builtin_amdgcn_readfirstlane(__shfl(ls.L, b));
   } else {
+    Cursor dummy;
+    S = locate<PG>(p, J, -1, &dummy);
     for (int b0 = 0; b0 < b; b0 += 64) {
       const int bb = b0 + lane;
-      const int Lb = bb < b ? clamp_len<PG>(p, p.context_lens[bb]) : 0;
+      const int Lb = bb < b ? len_lane<PG>(p, bb) : 0;
       int64_t t = (int64_t)((Lb + kSK - 1) / kSK) * J;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
       before += t;
     }
-    L = clamp_len<PG>(p, p.context_lens[b]);
+    L = len_lane<PG>(p, b);
   }
   const int nst = (L + kSK - 1) / kSK;
   T* out = static_cast<T*>(p.o) + (int64_t)bh * 128 + 2 * lane;
@@ -532,7 +729,7 @@ hipError_t launch_qr(const DecodeParams& p, hipStream_t st) {
 
 template <typename T>
 hipError_t launch_pg(const DecodeParams& p, bool paged, hipStream_t st) {
-  if (!paged) return p.context_lens != nullptr ? launch_qr<T, 1>(p, st) : launch_qr<T, 0>(p, st);
+  if (!paged) return p.positions != nullptr ? launch_qr<T, 1>(p, st) : launch_qr<T, 0>(p, st);
   if (p.page_size % 32 == 0) return launch_qr<T, 32>(p, st);
   return launch_qr<T, 4>(p, st);
 }

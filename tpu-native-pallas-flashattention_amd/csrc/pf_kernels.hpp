@@ -87,8 +87,7 @@ struct DecodeParams {
   const void* v;
   void* o;
   const int32_t* block_tables;  // null for the contiguous cache
-  const int32_t* context_lens;  // paged: [B] lengths; contiguous: null (cache_len
-                                // for every batch) or [B] lengths in device memory
+  const int32_t* context_lens;  // paged: [B] lengths; contiguous: null
   float* part_o;                // [B, Hq, n_split, D] partial (unnormalised) outputs
   float* part_ml;               // [B, Hq, n_split, 2] partial (max, sum)
   int B, Hq, Hkv, D;
@@ -100,6 +99,22 @@ struct DecodeParams {
   float scale_log2;
   int stages;         // streaming kernel: LDS ring depth (2..4)
   int n_waves;        // streaming kernel: persistent grid (one wave per workgroup)
+  // Fused decode step (streaming kernel, positions != null): the new token of
+  // batch b is at pos = positions[b * pos_stride]; its k (rotated with table
+  // row pos) and v go to cache slot pos (ring: pos % cache_size) and it
+  // attends pos + 1 (ring: min(pos + 1, cache_size)) slots; q is rotated with
+  // row pos too. An invalid position (negative; linear: >= cache_size; past
+  // rope_len with tables) attends nothing and writes nothing.
+  const int32_t* positions;
+  int pos_stride;
+  int ring;
+  const float* rope_cos;  // [rope_len, D] or null (no rotation)
+  const float* rope_sin;
+  int rope_len;
+  const void* k_new;  // [B, Hkv, D]
+  const void* v_new;
+  void* k_out;        // the cache again, writable (= k, v)
+  void* v_out;
 };
 
 // Split-KV partials + combine; picks the streaming kernel (decode_stream.hip)
@@ -136,26 +151,5 @@ struct PagedWriteParams {
   int B, Hkv, L, num_pages, page_size, pages_per_seq;
 };
 hipError_t launch_paged_cache_write(const PagedWriteParams& p, int dtype, int head_dim, hipStream_t stream);
-
-// Fused decode step: prologue (RoPE of q and the new k at the token's
-// position, cache-slot write, per-batch live length) before the streaming
-// decode over the device-side lengths.
-struct DecodeStepParams {
-  const void* q;      // [B, Hq, D] pre-RoPE query of the new token
-  const void* k_new;  // [B, Hkv, D] pre-RoPE key
-  const void* v_new;  // [B, Hkv, D]
-  void* k_cache;      // [B, Hkv, C, D]
-  void* v_cache;
-  void* q_rot;        // [B, Hq, D] workspace: rotated query
-  int32_t* kv_lens;   // [B] workspace: live keys per batch
-  const int32_t* positions;
-  int pos_stride;
-  const float* cos;   // [rope_len, D] or null (no rotation)
-  const float* sin;
-  int rope_len;
-  int B, Hq, Hkv, C;
-  int ring;
-};
-hipError_t launch_decode_step_prep(const DecodeStepParams& p, int dtype, int head_dim, hipStream_t stream);
 
 }  // namespace pf
