@@ -9,18 +9,25 @@ resident synthetic batch: pf_attn_fwd, then pf_attn_bwd_delta,
 pf_attn_bwd_dq and pf_attn_bwd_dkv, called through the C ABI on torch's
 current stream with HIP events between the launches (per-kernel durations).
 
-Secondary figures in the same line (each timed with HIP events):
+Secondary figures in the same line (each timed with HIP events; medians
+over the timed launches, after at least as many untimed ones as --warmup):
   fwd_tflops    config 3 forward alone (the pf_attn_fwd launches of the steps)
   rope_tflops   config 2 fused-RoPE prefill, bf16 causal GQA B=4 Hq=32 Hkv=8 S=4096
+                (K rotation + attention); fwd_cfg2_shape_ms is the plain forward
+                at that shape, timed in alternation (rope_over_plain_fwd)
   decode_gbs    config 4 decode, B=64 Hq=32 Hkv=8, cache 8192 with kv_len 6000
                 (slots past 6000 NaN); algorithmic bytes = valid K/V once + q + o
   decode_step_gbs  config 4's shape as one fused decode step (RoPE of the new
                 token at position 5999, cache-slot write, attention over 6000
-                slots; position in device memory)
+                slots; position in device memory), timed in alternation with
+                the config 4 decode on the same cache
   paged_gbs     config 5 paged decode, 128 seqs, page 64, lens U[512, 8192] from
                 np.random.default_rng(0), 16384-page pool, -1-padded table,
                 unreferenced pages and tails NaN; bytes = valid K/V + q + o +
                 used table entries + lens
+  hbm_read_ceiling_gbs  a plain streaming read of 2 GiB (the best of a few
+                launch shapes): what a read-only HBM stream reaches on this
+                device; *_frac_read_ceiling relate decode/paged to it
 
 Synthetic inputs: N(0,1) from torch's CUDA generator seeded 0 (config 5's
 lengths and page permutation from numpy's default_rng(0)), cast to bf16.
@@ -79,6 +86,9 @@ class Events:
     def mean_ms(self, j0: int, j1: int) -> float:
         return float(np.mean([e[j0].elapsed_time(e[j1]) for e in self.ev]))
 
+    def median_ms(self, j0: int, j1: int) -> float:
+        return float(np.median([e[j0].elapsed_time(e[j1]) for e in self.ev]))
+
 
 def ok(status: int, what: str):
     if status != 0:
@@ -132,7 +142,7 @@ def bench_cfg3(L, _lib, torch, steps, warmup):
                 host=host)
 
 
-def bench_rope(L, _lib, torch, iters):
+def bench_rope(L, _lib, torch, iters, warmup):
     from pallas_flash import precompute_rope
     B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
     g = torch.Generator(device="cuda").manual_seed(1)
@@ -145,17 +155,27 @@ def bench_rope(L, _lib, torch, iters):
     ra = _lib.FwdRopeArgs(base, cos.data_ptr(), sin.data_ptr(), cos.data_ptr(), sin.data_ptr(), None, 0)
     ws = torch.empty(L.pf_attn_fwd_rope_workspace_size(ra), dtype=torch.uint8, device="cuda")
     ra.workspace, ra.workspace_bytes = ws.data_ptr(), ws.numel()
+    # the plain forward at the same shape (no LSE, as the fused kernel), timed
+    # in alternation: what the rotation costs
+    o2 = torch.empty_like(q)
+    plain = _lib.FwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o2.data_ptr(), None,
+                         B, Hq, Hkv, S, S, D, S, 1, 1.0 / D ** 0.5, 1)
     st = torch.cuda.current_stream().cuda_stream
-    for _ in range(3):
-        ok(L.pf_attn_fwd_rope(ra, st), "pf_attn_fwd_rope")
-    ev = Events(2, iters)
+    run = {"rope": lambda: ok(L.pf_attn_fwd_rope(ra, st), "pf_attn_fwd_rope"),
+           "plain": lambda: ok(L.pf_attn_fwd(plain, st), "pf_attn_fwd")}
+    for _ in range(max(3, warmup)):
+        for f in run.values():
+            f()
+    ev = {k_: Events(2, iters) for k_ in run}
     for i in range(iters):
-        ev.mark(i, 0)
-        ok(L.pf_attn_fwd_rope(ra, st), "pf_attn_fwd_rope")
-        ev.mark(i, 1)
+        for k_, f in run.items():
+            ev[k_].mark(i, 0)
+            f()
+            ev[k_].mark(i, 1)
     torch.cuda.synchronize()
-    ms = ev.mean_ms(0, 1)
-    return ms, fwd_flops(B, Hq, D, causal_pairs(S)), {"q": q, "k": k, "v": v, "cos": cos, "sin": sin}
+    ms = ev["rope"].median_ms(0, 1)
+    plain_ms = ev["plain"].median_ms(0, 1)
+    return ms, plain_ms, fwd_flops(B, Hq, D, causal_pairs(S)), {"q": q, "k": k, "v": v, "cos": cos, "sin": sin}
 
 
 def _decode_args_and_ws(L, _lib, torch, args, size_fn):
@@ -166,8 +186,16 @@ def _decode_args_and_ws(L, _lib, torch, args, size_fn):
     return ws
 
 
-def bench_decode(L, _lib, torch, iters):
+def bench_decode(L, _lib, torch, iters, warmup):
+    """Config 4 decode (pf_attn_decode) and, on the same cache, config 4's
+    shape as one fused decode step (pf_attn_decode_step: RoPE of the new
+    token's q/k at position 5999, cache-slot write, attention over the 6000
+    live slots, position in device memory). The two are timed in alternation
+    (same clocks, same cache); medians. Step bytes = the decode bytes + the
+    new k/v rows read and written + the two table rows."""
+    from pallas_flash import precompute_rope
     B, Hq, Hkv, cap, D, kv_len = 64, 32, 8, 8192, 128, 6000
+    pos = kv_len - 1
     g = torch.Generator(device="cuda").manual_seed(2)
     q = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
     kc = torch.empty((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda")
@@ -175,66 +203,41 @@ def bench_decode(L, _lib, torch, iters):
     for t in (kc, vc):
         t[:, :, :kv_len].copy_(torch.randn((B, Hkv, kv_len, D), generator=g, device="cuda"))
         t[:, :, kv_len:].fill_(float("nan"))
-    o = torch.empty_like(q)
+    kn = torch.randn((B, Hkv, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    vn = torch.randn((B, Hkv, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    cos, sin = precompute_rope(cap, D, 10000.0, device="cuda")
+    positions = torch.full((B,), pos, dtype=torch.int32, device="cuda")
+    o, o_step = torch.empty_like(q), torch.empty_like(q)
     args = _lib.DecodeArgs(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), B, Hq, Hkv, cap,
                            D, kv_len, 1.0 / D ** 0.5, 1, None, 0)
     ws = _decode_args_and_ws(L, _lib, torch, args, L.pf_attn_decode_workspace_size)
+    sargs = _lib.DecodeStepArgs(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                o_step.data_ptr(), positions.data_ptr(), 1, cos.data_ptr(), sin.data_ptr(), cap,
+                                B, Hq, Hkv, cap, D, 0, 1.0 / D ** 0.5, 1, None, 0)
+    ws_step = _decode_args_and_ws(L, _lib, torch, sargs, L.pf_attn_decode_step_workspace_size)
     st = torch.cuda.current_stream().cuda_stream
-    for _ in range(3):
-        ok(L.pf_attn_decode(args, st), "pf_attn_decode")
-    ev = Events(2, iters)
+    run = {"decode": lambda: ok(L.pf_attn_decode(args, st), "pf_attn_decode"),
+           "step": lambda: ok(L.pf_attn_decode_step(sargs, st), "pf_attn_decode_step")}
+    for _ in range(max(3, warmup)):
+        for f in run.values():
+            f()
+    ev = {k: Events(2, iters) for k in run}
     for i in range(iters):
-        ev.mark(i, 0)
-        ok(L.pf_attn_decode(args, st), "pf_attn_decode")
-        ev.mark(i, 1)
+        for k, f in run.items():
+            ev[k].mark(i, 0)
+            f()
+            ev[k].mark(i, 1)
     torch.cuda.synchronize()
     assert torch.isfinite(o.float()).all(), "decode output not finite"
+    assert torch.isfinite(o_step.float()).all(), "decode step output not finite"
     nbytes = B * Hkv * kv_len * D * 2 * 2 + 2 * B * Hq * D * 2
-    del ws
-    return ev.mean_ms(0, 1), nbytes, {"q": q, "k": kc, "v": vc, "kv_len": kv_len}
+    nbytes_step = nbytes + 2 * 2 * B * Hkv * D * 2 + 2 * D * 4
+    del ws, ws_step
+    return ({"decode": (ev["decode"].median_ms(0, 1), nbytes), "step": (ev["step"].median_ms(0, 1), nbytes_step)},
+            {"q": q, "k": kc, "v": vc, "kv_len": kv_len})
 
 
-def bench_decode_step(L, _lib, torch, iters):
-    """Config 4's shape as a fused decode step (pf_attn_decode_step): RoPE of
-    the new token's q/k at position 5999, cache-slot write, attention over the
-    6000 live slots (device-side position). Bytes = the config-4 decode bytes
-    + the new k/v rows read and written + the two table rows."""
-    from pallas_flash import precompute_rope
-    B, Hq, Hkv, cap, D, pos = 64, 32, 8, 8192, 128, 5999
-    g = torch.Generator(device="cuda").manual_seed(4)
-    q = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
-    kn = torch.randn((B, Hkv, 1, D), generator=g, device="cuda").to(torch.bfloat16)
-    vn = torch.randn((B, Hkv, 1, D), generator=g, device="cuda").to(torch.bfloat16)
-    kc = torch.empty((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda")
-    vc = torch.empty_like(kc)
-    for t in (kc, vc):
-        t[:, :, :pos].copy_(torch.randn((B, Hkv, pos, D), generator=g, device="cuda"))
-        t[:, :, pos:].fill_(float("nan"))
-    cos, sin = precompute_rope(cap, D, 10000.0, device="cuda")
-    positions = torch.full((B,), pos, dtype=torch.int32, device="cuda")
-    o = torch.empty_like(q)
-    args = _lib.DecodeStepArgs(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                               o.data_ptr(), positions.data_ptr(), 1, cos.data_ptr(), sin.data_ptr(), cap,
-                               B, Hq, Hkv, cap, D, 0, 1.0 / D ** 0.5, 1, None, 0)
-    ws = _decode_args_and_ws(L, _lib, torch, args, L.pf_attn_decode_step_workspace_size)
-    st = torch.cuda.current_stream().cuda_stream
-    for _ in range(3):
-        ok(L.pf_attn_decode_step(args, st), "pf_attn_decode_step")
-    ev = Events(2, iters)
-    for i in range(iters):
-        ev.mark(i, 0)
-        ok(L.pf_attn_decode_step(args, st), "pf_attn_decode_step")
-        ev.mark(i, 1)
-    torch.cuda.synchronize()
-    assert torch.isfinite(o.float()).all(), "decode step output not finite"
-    kv_len = pos + 1
-    nbytes = (B * Hkv * kv_len * D * 2 * 2 + 2 * B * Hq * D * 2 + 2 * 2 * B * Hkv * D * 2
-              + 2 * D * 4)
-    del ws
-    return ev.mean_ms(0, 1), nbytes
-
-
-def bench_paged(L, _lib, torch, iters):
+def bench_paged(L, _lib, torch, iters, warmup):
     B, Hq, Hkv, D, page, npages, pps = 128, 32, 8, 128, 64, 16384, 128
     rng = np.random.default_rng(0)
     lens = rng.integers(512, 8193, B)
@@ -266,7 +269,7 @@ def bench_paged(L, _lib, torch, iters):
                           o.data_ptr(), B, Hq, Hkv, npages, page, D, pps, 1.0 / D ** 0.5, 1, None, 0)
     ws = _decode_args_and_ws(L, _lib, torch, args, L.pf_paged_attn_workspace_size)
     st = torch.cuda.current_stream().cuda_stream
-    for _ in range(3):
+    for _ in range(max(3, warmup)):
         ok(L.pf_paged_attn(args, st), "pf_paged_attn")
     ev = Events(2, iters)
     for i in range(iters):
@@ -278,7 +281,45 @@ def bench_paged(L, _lib, torch, iters):
     npg = -(-lens // page)
     nbytes = int(lens.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2 + 4 * int(npg.sum()) + 4 * B
     del ws
-    return ev.mean_ms(0, 1), nbytes, {"q": q, "k": kp, "v": vp, "table": table, "lens": lens}
+    return ev.median_ms(0, 1), nbytes, {"q": q, "k": kp, "v": vp, "table": table, "lens": lens}
+
+
+def bench_read_ceiling(torch, iters):
+    """The practical HBM read ceiling: a plain streaming read of a 2 GiB
+    buffer (16-byte non-temporal loads, 4 or 8 in flight per thread,
+    grid-stride over 2048-16384 workgroups of 256 threads; the probe library
+    built beside the attention library). The best configuration's median
+    time. Returns (GB/s, description)."""
+    import ctypes
+    path = os.path.join(PKG_DIR, "pallas_flash", "libpf_bench_probe.so")
+    probe = ctypes.CDLL(path)
+    fn = probe.pf_probe_stream_read
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    nbytes = 2 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    sink = torch.zeros(16384, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    best = None
+    for unroll in (4, 8):
+        for blocks in (2048, 4096, 8192, 16384):
+            call = lambda: ok(fn(buf.data_ptr(), nbytes, sink.data_ptr(), blocks, unroll, st), "probe read")
+            for _ in range(3):
+                call()
+            ev = Events(2, iters)
+            for i in range(iters):
+                ev.mark(i, 0)
+                call()
+                ev.mark(i, 1)
+            torch.cuda.synchronize()
+            ms = float(np.median([e[0].elapsed_time(e[1]) for e in ev.ev]))
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            if best is None or gbs > best[0]:
+                best = (gbs, f"{blocks} workgroups x 256 threads, {unroll} 16-byte non-temporal loads in flight "
+                             f"per thread, 2 GiB buffer, median of {iters}")
+    del buf, sink
+    return best
 
 
 def bench_copy(torch, iters):
@@ -436,7 +477,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "step", "paged", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "stream", "copy"],
+                    default="all")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -461,36 +503,43 @@ def main():
     cpu_sec = {}
     if args.only in ("all", "rope"):
         log("cfg2 rope ...")
-        ms, F, rin = bench_rope(L, _lib, torch, iters)
+        ms, plain_ms, F, rin = bench_rope(L, _lib, torch, iters, args.warmup)
         sec["rope_tflops"] = F / (ms * 1e-3) / 1e12
         sec["rope_ms"] = ms
+        sec["fwd_cfg2_shape_ms"] = plain_ms
+        sec["rope_over_plain_fwd"] = ms / plain_ms
         if not args.skip_cpu:
             log("cpu baseline cfg2 ...")
             cpu_sec["rope"] = cpu_baseline_rope(rin)
         del rin
     if args.only in ("all", "decode"):
-        log("cfg4 decode ...")
-        ms, nb, din = bench_decode(L, _lib, torch, iters)
+        log("cfg4 decode and decode step ...")
+        res, din = bench_decode(L, _lib, torch, iters, args.warmup)
+        ms, nb = res["decode"]
         sec["decode_gbs"] = nb / (ms * 1e-3) / 1e9
         sec["decode_ms"] = ms
+        ms, nb = res["step"]
+        sec["decode_step_gbs"] = nb / (ms * 1e-3) / 1e9
+        sec["decode_step_ms"] = ms
         if not args.skip_cpu:
             log("cpu baseline cfg4 ...")
             cpu_sec["decode"] = cpu_baseline_decode(din)
         del din
-    if args.only in ("all", "step"):
-        log("cfg4-shape decode step ...")
-        ms, nb = bench_decode_step(L, _lib, torch, iters)
-        sec["decode_step_gbs"] = nb / (ms * 1e-3) / 1e9
-        sec["decode_step_ms"] = ms
     if args.only in ("all", "paged"):
         log("cfg5 paged ...")
-        ms, nb, pin = bench_paged(L, _lib, torch, iters)
+        ms, nb, pin = bench_paged(L, _lib, torch, iters, args.warmup)
         sec["paged_gbs"] = nb / (ms * 1e-3) / 1e9
         sec["paged_ms"] = ms
         if not args.skip_cpu:
             log("cpu baseline cfg5 ...")
             cpu_sec["paged"] = cpu_baseline_paged(pin)
         del pin
+
+    if args.only in ("all", "stream"):
+        log("hbm read ceiling ...")
+        gbs, how = bench_read_ceiling(torch, iters)
+        sec["hbm_read_ceiling_gbs"] = gbs
+        sec["hbm_read_ceiling_config"] = how
 
     if args.only == "copy":
         log("copy calibration ...")
@@ -529,6 +578,10 @@ def main():
         line["secondary"]["decode_step_frac_hbm"] = round(sec["decode_step_gbs"] / PEAK_HBM_GBS, 4)
     if "paged_gbs" in sec:
         line["secondary"]["paged_frac_hbm"] = round(sec["paged_gbs"] / PEAK_HBM_GBS, 4)
+    if "hbm_read_ceiling_gbs" in sec:
+        for k in ("decode", "decode_step", "paged"):
+            if f"{k}_gbs" in sec:
+                line["secondary"][f"{k}_frac_read_ceiling"] = round(sec[f"{k}_gbs"] / sec["hbm_read_ceiling_gbs"], 4)
     if "fwd_tflops" in sec:
         line["secondary"]["fwd_frac_mfma"] = round(sec["fwd_tflops"] / PEAK_BF16_TFLOPS, 4)
     if cpu_sec:
