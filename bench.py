@@ -5,9 +5,10 @@ Headline ("value"): flash_attention forward+backward at BASELINE config 3
 (bf16, causal, GQA, B=2, Hq=16, Hkv=4, S=8192, D=128) in algorithmic
 TFLOP/s: 4*B*Hq*D*S(S+1)/2 per forward, x3.5 for forward+backward
 (recomputation not credited). One step = one forward + backward over the
-resident synthetic batch: pf_attn_fwd, then pf_attn_bwd_delta,
-pf_attn_bwd_dq and pf_attn_bwd_dkv, called through the C ABI on torch's
-current stream with HIP events between the launches (per-kernel durations).
+resident synthetic batch: pf_attn_fwd, then pf_attn_bwd_dq (which also
+computes delta = rowsum(o * do)) and pf_attn_bwd_dkv, called through the C
+ABI on torch's current stream with HIP events between the launches
+(per-kernel durations).
 
 Secondary figures in the same line (each timed with HIP events; medians
 over the timed launches, after at least as many untimed ones as --warmup):
@@ -116,24 +117,22 @@ def bench_cfg3(L, _lib, torch, steps, warmup):
         if ev: ev.mark(it, 0)
         ok(L.pf_attn_fwd(fa, st), "pf_attn_fwd")
         if ev: ev.mark(it, 1)
-        ok(L.pf_attn_bwd_delta(ba, st), "pf_attn_bwd_delta")
+        ok(L.pf_attn_bwd_dq(ba, st), "pf_attn_bwd_dq")  # also writes delta
         if ev: ev.mark(it, 2)
-        ok(L.pf_attn_bwd_dq(ba, st), "pf_attn_bwd_dq")
-        if ev: ev.mark(it, 3)
         ok(L.pf_attn_bwd_dkv(ba, st), "pf_attn_bwd_dkv")
-        if ev: ev.mark(it, 4)
+        if ev: ev.mark(it, 3)
 
     for _ in range(warmup):
         step()
-    ev = Events(5, steps)
+    ev = Events(4, steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         step(ev, i)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    kern_ms = {"pf_attn_fwd_kernel": ev.mean_ms(0, 1), "pf_attn_bwd_delta_kernel": ev.mean_ms(1, 2),
-               "pf_attn_bwd_dq_kernel": ev.mean_ms(2, 3), "pf_attn_bwd_dkv_kernel": ev.mean_ms(3, 4)}
+    kern_ms = {"pf_attn_fwd_kernel": ev.mean_ms(0, 1), "pf_attn_bwd_dq_kernel": ev.mean_ms(1, 2),
+               "pf_attn_bwd_dkv_kernel": ev.mean_ms(2, 3)}
     F = fwd_flops(B, Hq, D, causal_pairs(S))
     # algorithmic credit per launch: fwd = 2 matmuls; dkv = S, dP, dV, dK (4); dq = dQ (1)
     credit = {"pf_attn_fwd_kernel": F, "pf_attn_bwd_dq_kernel": 0.5 * F, "pf_attn_bwd_dkv_kernel": 2.0 * F}

@@ -145,8 +145,11 @@ int pf_rope(const pf_rope_args* args, void* stream);
  *   q, o, do_, dq [batch, num_heads,    seq_len_q, head_dim]  (dtype)
  *   k, v, dk, dv  [batch, num_kv_heads, seq_len_k, head_dim]  (dtype)
  *   lse           [batch, num_heads, seq_len_q] float32 (from pf_attn_fwd)
- *   delta         [batch, num_heads, seq_len_q] float32 workspace; written by
- *                 pf_attn_bwd_delta, read by the dq / dkv kernels.
+ *   delta         [batch, num_heads, seq_len_q] float32 workspace, the
+ *                 rowsum of o * do_: written by pf_attn_bwd_delta and (from
+ *                 its own rows) by pf_attn_bwd_dq, read by pf_attn_bwd_dkv --
+ *                 so dkv runs after either of the two; pf_attn_bwd runs dq,
+ *                 then dkv.
  * dk/dv are summed over the num_heads/num_kv_heads query heads of each group in
  * float32 before the single cast to dtype. Keys >= kv_len get zero gradient.
  * ------------------------------------------------------------------------- */
@@ -171,7 +174,7 @@ typedef struct {
 int pf_attn_bwd_delta(const pf_attn_bwd_args* args, void* stream);
 int pf_attn_bwd_dq(const pf_attn_bwd_args* args, void* stream);
 int pf_attn_bwd_dkv(const pf_attn_bwd_args* args, void* stream);
-/* delta, then dq and dkv, on one stream */
+/* dq (which also writes delta), then dkv, on one stream */
 int pf_attn_bwd(const pf_attn_bwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -133,3 +133,42 @@ def test_bf16_grads_keep_dtype_and_finite():
     for t in (tq, tk, tv):
         assert t.grad.dtype == torch.bfloat16
         assert torch.isfinite(t.grad.float()).all()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_delta_entry_point_and_dq_agree(dt):
+    """delta = rowsum(o * do) (flash_attention.py:363-365) from the stored
+    output: pf_attn_bwd_delta and the value pf_attn_bwd_dq writes (it computes
+    delta for its own rows) both match the float64 rowsum; the three C-ABI
+    launches delta -> dq -> dkv and the combined pf_attn_bwd (dq -> dkv) give
+    the same gradients."""
+    from pallas_flash import _lib, flash_attention_with_lse
+    note(f"bwd delta entry points {dt}")
+    rng = np.random.default_rng(31)
+    B, Hq, Hkv, S, D = 2, 4, 2, 192, 128
+    q, k, v, do = (dev(rng.standard_normal(s), dt) for s in
+                   ((B, Hq, S, D), (B, Hkv, S, D), (B, Hkv, S, D), (B, Hq, S, D)))
+    o, lse = flash_attention_with_lse(q, k, v, causal=True)
+    want = (host(o) * host(do)).sum(-1)
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(order):
+        delta = torch.full((B, Hq, S), float("nan"), dtype=torch.float32, device="cuda")
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        a = _lib.BwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+                         delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, S, S, D, S, 1,
+                         D ** -0.5, _lib.dtype_tag(q))
+        for name in order:
+            assert getattr(L, name)(a, st) == _lib.PF_OK, name
+        torch.cuda.synchronize()
+        return host(delta), host(dq), host(dk), host(dv)
+
+    d_only = run(["pf_attn_bwd_delta"])[0]
+    d_dq = run(["pf_attn_bwd_dq"])[0]
+    tol = 1e-5 * np.abs(want).max()
+    assert np.abs(d_only - want).max() <= tol and np.abs(d_dq - want).max() <= tol
+    split = run(["pf_attn_bwd_delta", "pf_attn_bwd_dq", "pf_attn_bwd_dkv"])
+    fused = run(["pf_attn_bwd"])
+    for name, x, y in zip(("dq", "dk", "dv"), split[1:], fused[1:]):
+        assert rel_err(x, y) <= (1e-5 if dt == "f32" else 2e-2), name

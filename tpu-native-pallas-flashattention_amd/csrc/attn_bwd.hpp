@@ -17,7 +17,8 @@
 // bounds-checked buffer loads, double-buffered with one barrier per step, and
 // every transposed operand read from the single natural copy with the
 // transposing LDS load (pf_tiles.hpp).
-//  dQ (workgroup = 128 query rows, 4 waves x 32 rows; loop over 64-key blocks):
+//  dQ (workgroup = 128 query rows, 4 waves x 32 rows; loop over 64-key blocks;
+//  it also computes delta for its rows and stores it for dK/dV):
 //    S^T = K Q^T, dP^T = V dO^T  (K, V tiles; Q, dO in registers)
 //    dS^T = P^T (dP^T - delta);  dQ^T += K^T dS^T  (K^T from the K tile)
 //  dK/dV (workgroup = 128 keys, 4 waves x 32 keys; loop over the group's
@@ -101,7 +102,31 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   load_row_frags<T, D>(Qb, qrow, qvalid, hh, qf);
   load_row_frags<T, D>(dOb, qrow, qvalid, hh, dof);
   const float lse2 = qvalid ? p.lse[qoff + qrow] * kLog2e : 0.f;
-  const float dlt = qvalid ? p.delta[qoff + qrow] : 0.f;
+  // delta = sum_d f32(o) f32(do) of this row from the stored output
+  // (flash_attention.py:363-365): each lane half sums its half of the row,
+  // one exchange adds the two. Written for the dK/dV kernel, which runs
+  // after this one.
+  float dlt;
+  {
+    constexpr int EPC = 16 / (int)sizeof(T), FPC = frags_per_chunk<T>();
+    const T* orow = static_cast<const T*>(p.o) + (qoff + (qvalid ? qrow : 0)) * D + hh * (D / 2);
+    float part = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 2 / EPC; ++c) {
+      float a[EPC], d[EPC];
+      chunk_to_f32<T>(ldg16(orow + c * EPC), a);
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int f = 0; f < FPC; ++f) d[f] = dof[c * FPC + f];
+      } else {
+        chunk_to_f32<T>(__builtin_bit_cast(u32x4, dof[c]), d);
+      }
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) part += a[e] * d[e];
+    }
+    dlt = qvalid ? wave_xor32_sum(part) : 0.f;
+    if (qvalid && hh == 0) p.delta[qoff + qrow] = dlt;
+  }
 
   f32x16 acc[NDT];
 #pragma unroll

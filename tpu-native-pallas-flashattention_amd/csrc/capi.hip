@@ -243,8 +243,7 @@ int pf_attn_bwd(const pf_attn_bwd_args* a, void* stream) {
   if (st != PF_OK) return st;
   hipStream_t s = (hipStream_t)stream;
   if ((int64_t)p.B * p.Hq * p.Sq > 0) {
-    st = finish(pf::launch_attn_bwd_delta(p, a->dtype, a->head_dim, s));
-    if (st != PF_OK) return st;
+    // the dQ kernel computes delta itself and stores it for dK/dV
     st = finish(pf::launch_attn_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, s));
     if (st != PF_OK) return st;
   }
