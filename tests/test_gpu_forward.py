@@ -170,3 +170,21 @@ def test_nondefault_stream_and_device_guard():
     s.synchronize()
     ref, _ = attention_ref(host(tq), host(tk), host(tv), causal=True)
     assert rel_err(host(out), ref) < 1e-5
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(2, 16, 8, 300), (4, 64, 8, 160), (1, 16, 16, 200), (3, 24, 8, 96)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_pair_grouped_work_order(B, Hq, Hkv, S, causal):
+    """(batch, kv head) pairs a multiple of 8 and more than 8: each XCD runs
+    its pairs in L2-sized groups (fwd_work_item). Every row of o and LSE must
+    still be produced exactly once and match the oracle (GQA group sizes 2,
+    8, 1 and 3; ragged query blocks)."""
+    note(f"pair-grouped order B={B} Hq={Hq} Hkv={Hkv} S={S} causal={causal}")
+    rng = np.random.default_rng(B * 100 + Hq)
+    q, k, v = qkv(rng, B, Hq, Hkv, S, S)
+    tq, tk, tv = dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16")
+    out, lse = flash_attention_with_lse(tq, tk, tv, causal=causal)
+    torch.cuda.synchronize()
+    ref, ref_lse = attention_ref(host(tq), host(tk), host(tv), causal=causal)
+    check_fwd(host(out), ref, "bf16")
+    assert max_abs(host(lse), ref_lse) <= 1e-3

@@ -70,6 +70,25 @@ int fwd_rows_per_wave(const pf_attn_fwd_args* a) {
   return tuning().fwd_rows_per_wave.load(std::memory_order_relaxed) == 64 ? 64 : 32;
 }
 
+// (batch, kv head) pairs each XCD streams at a time in the forward
+// (fwd_work_item): with more than one pair per XCD, the largest divisor of
+// the per-XCD pair count whose pairs' live K/V (kv_len rows each) fits an
+// XCD's 4 MB L2, at least 1; 0 (the default item order) when the pairs are
+// not a multiple of the 8 XCDs or one pair per XCD. (Config 2's shape, four
+// 2 MiB pairs per XCD: two at a time measured 1.5% faster than one and as
+// fast as all four, with half of their HBM traffic.)
+int fwd_pair_group(const pf_attn_fwd_args* a) {
+  const int64_t npairs = (int64_t)a->batch * a->num_kv_heads;
+  if (npairs % 8 != 0 || npairs == 8) return 0;
+  const int per_xcd = (int)(npairs / 8);
+  const int64_t es = a->dtype == PF_DTYPE_F32 ? 4 : 2;
+  const int64_t pair_bytes = (int64_t)a->kv_len * a->head_dim * es * 2;
+  int best = 1;
+  for (int P = 1; P <= per_xcd; ++P)
+    if (per_xcd % P == 0 && P * pair_bytes <= (int64_t)(4 << 20)) best = P;
+  return best;
+}
+
 int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   int st = check_attn_dims(a->batch, a->num_heads, a->num_kv_heads, a->seq_len_q, a->seq_len_k,
                            a->head_dim, a->kv_len, a->sm_scale, a->dtype);
@@ -100,6 +119,7 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   // per-(batch, kv head) byte offsets are 32-bit inside the kernels
   if ((int64_t)(a->seq_len_k + 256) * a->head_dim * 4 > 0x7fffffff) return PF_ERR_UNSUPPORTED;
   p->n_work = (int)n_work;
+  p->pair_group = fwd_pair_group(a);
   return PF_OK;
 }
 

@@ -26,16 +26,35 @@ struct FwdParams {
   int rpw;           // query rows per head per workgroup (4 * rows_per_wave / hpw)
   int n_qblk;        // ceil(Sq / rpw)
   int n_work;        // B * Hq / hpw * n_qblk
+  int pair_group;    // > 0: (batch, kv head) pairs an XCD streams at a time (fwd_work_item)
 };
 
 // Work item of forward workgroup `bid`: (batch b, kv head kvh, head group hg
-// of the GQA group, query block qblk). Items run in (query block, batch, kv
-// head, head group) order, heavy (late, causal) query blocks first, with the
-// head groups of one kv head on one XCD (xcd_remap: workgroups are
-// dispatched round-robin over the 8 XCDs, each with its own L2). A bijection
-// of [0, n_work).
+// of the GQA group, query block qblk). Workgroups are dispatched round-robin
+// over the 8 XCDs (XCD = bid % 8), each with its own L2, and start on an XCD
+// in bid order. Items are issued heavy (late, causal) query blocks first.
+//  * When the (batch, kv head) pairs are a multiple of 8 and p.pair_group
+//    (P) is set, each XCD owns pairs xcd, xcd + 8, ... and runs them P at a
+//    time, the P pairs' items interleaved: the workgroups resident on an XCD
+//    then stream P pairs' K/V, which the host sizes to fit its L2.
+//  * Otherwise items run in (query block, batch, kv head, head group) order
+//    with the head groups of one kv head on one XCD (xcd_remap).
+// Both are bijections of [0, n_work).
 __device__ inline void fwd_work_item(int bid, const FwdParams& p, int& b, int& kvh, int& hg, int& qblk) {
   const int n_hg = p.g / p.hpw;
+  if (p.pair_group > 0) {
+    const int per_pair = p.n_qblk * n_hg;
+    const int P = p.pair_group;
+    const int xcd = bid & 7, slot = bid >> 3;
+    const int grp = slot / (P * per_pair), r = slot - grp * (P * per_pair);
+    const int pair = (grp * P + r % P) * 8 + xcd;
+    const int it = r / P;  // item within the pair
+    hg = it % n_hg;
+    qblk = p.n_qblk - 1 - it / n_hg;
+    kvh = pair % p.Hkv;
+    b = pair / p.Hkv;
+    return;
+  }
   const int w = xcd_remap(bid, p.n_work, n_hg);
   hg = w % n_hg;
   int rest = w / n_hg;
