@@ -465,10 +465,13 @@ def load_traffic(kernel: str, workload: str):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            rec = json.load(f).get(workload, {}).get(kernel)
+            recs = json.load(f).get(workload, {})
     except (OSError, ValueError):
         return None
-    return None if rec is None else int(rec["bytes"])
+    # keys are kernel names with their template arguments ("name<bf16, 128, ...>");
+    # the workload runs one instantiation of each kernel
+    hits = [r for k, r in recs.items() if k == kernel or k.startswith(kernel + "<")]
+    return int(hits[0]["bytes"]) if len(hits) == 1 else None
 
 
 def main():
