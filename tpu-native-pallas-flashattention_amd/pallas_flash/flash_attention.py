@@ -10,8 +10,9 @@ reached through the C ABI in ``include/pallas_flash_amd.h``.
 * ``flash_attention`` is differentiable in q, k and v (a
   ``torch.autograd.Function``, the counterpart of the reference's
   ``jax.custom_vjp`` at flash_attention.py:448-476). Its backward runs the
-  delta, dQ and dK/dV kernels; dK/dV are summed over each GQA group in float32
-  before the cast to the input dtype (flash_attention.py:433-442).
+  dQ kernel (which also writes delta = rowsum(o * do)) and then the dK/dV
+  kernel; dK/dV are summed over each GQA group in float32 before the cast to
+  the input dtype (flash_attention.py:433-442).
 * ``flash_attention_decode`` (flash_attention.py:555-589) runs a split-KV
   decode kernel that reads each cached K/V byte once. When a gradient is
   requested it routes through ``flash_attention`` instead, as the reference
@@ -19,7 +20,9 @@ reached through the C ABI in ``include/pallas_flash_amd.h``.
 
 ``block_q``/``block_k`` are accepted for signature compatibility; tile shapes
 are chosen by the kernels. ``interpret`` is accepted and ignored: there is no
-CPU interpreter here, the HIP kernels always run.
+CPU interpreter here, the HIP kernels always run. Any head_dim up to 128 and
+any mix of input dtypes are accepted (``_shape``: zero-padding to the kernels'
+head_dim, float32 compute for mixed dtypes, output in q's dtype).
 """
 
 from __future__ import annotations
@@ -29,6 +32,7 @@ from typing import Optional
 import torch
 
 from . import _lib
+from ._shape import adapt, compute_dtype, kernel_head_dim, restore
 
 
 def _validate(q, k, v, kv_len):
@@ -49,8 +53,6 @@ def _validate(q, k, v, kv_len):
         kv_len = seq_len_k
     elif not 0 < kv_len <= seq_len_k:
         raise ValueError(f"kv_len must be in (0, {seq_len_k}], got {kv_len}")
-    if q.dtype != k.dtype or q.dtype != v.dtype:
-        raise ValueError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
     return int(kv_len)
 
 
@@ -138,15 +140,17 @@ def flash_attention(
 
     Returns:
         ``[batch, num_heads, seq_len_q, head_dim]`` in q's dtype. Differentiable
-        in q, k, v.
+        in q, k, v (gradients in each input's dtype).
     """
     kv_len = _validate(q, k, v, kv_len)
     head_dim = q.shape[3]
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
     _lib.require_device(q, k, v)
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    return _FlashAttentionFn.apply(q, k, v, bool(causal), float(sm_scale), kv_len)
+    cdt, dp = compute_dtype(q, k, v), kernel_head_dim(head_dim)
+    q2, k2, v2 = (adapt(x, cdt, dp).contiguous() for x in (q, k, v))
+    o = _FlashAttentionFn.apply(q2, k2, v2, bool(causal), float(sm_scale), kv_len)
+    return restore(o, head_dim, q.dtype)
 
 
 def flash_attention_with_lse(q, k, v, *, causal=False, sm_scale=None, kv_len=None):
@@ -154,11 +158,14 @@ def flash_attention_with_lse(q, k, v, *, causal=False, sm_scale=None, kv_len=Non
     (the residual the reference's forward kernel emits, flash_attention.py:
     192-194, 213; natural log of the scaled scores)."""
     kv_len = _validate(q, k, v, kv_len)
+    head_dim = q.shape[3]
     if sm_scale is None:
-        sm_scale = 1.0 / (q.shape[3] ** 0.5)
+        sm_scale = 1.0 / (head_dim ** 0.5)
     _lib.require_device(q, k, v)
-    return _fwd(q.contiguous(), k.contiguous(), v.contiguous(), bool(causal), float(sm_scale),
-                kv_len, True)
+    cdt, dp = compute_dtype(q, k, v), kernel_head_dim(head_dim)
+    q2, k2, v2 = (adapt(x, cdt, dp).contiguous() for x in (q, k, v))
+    o, lse = _fwd(q2, k2, v2, bool(causal), float(sm_scale), kv_len, True)
+    return restore(o, head_dim, q.dtype), lse
 
 
 def _decode(q, k_cache, v_cache, cache_len: int, sm_scale: float):
@@ -209,11 +216,13 @@ def flash_attention_decode(
         return flash_attention(q, k_cache, v_cache, causal=False, sm_scale=sm_scale, block_q=1,
                                block_k=block_k, kv_len=cache_len, interpret=interpret)
     cache_len = _validate(q, k_cache, v_cache, cache_len)
+    head_dim = q.shape[3]
     if sm_scale is None:
-        sm_scale = 1.0 / (q.shape[3] ** 0.5)
+        sm_scale = 1.0 / (head_dim ** 0.5)
     _lib.require_device(q, k_cache, v_cache)
-    return _decode(q.contiguous(), k_cache.contiguous(), v_cache.contiguous(), cache_len,
-                   float(sm_scale))
+    cdt, dp = compute_dtype(q, k_cache, v_cache), kernel_head_dim(head_dim)
+    q2, k2, v2 = (adapt(x, cdt, dp).contiguous() for x in (q, k_cache, v_cache))
+    return restore(_decode(q2, k2, v2, cache_len, float(sm_scale)), head_dim, q.dtype)
 
 
 __all__ = ["flash_attention", "flash_attention_decode", "flash_attention_with_lse"]

@@ -20,6 +20,9 @@ rotation).
 Numerics: the rotated Q and K are rounded once to the input dtype before the
 bf16/f16 MFMA (the reference keeps them in float32 and runs a float32 dot,
 fused_rope.py:75-78); float32 inputs keep float32 throughout.
+
+head_dim below 128 other than 64 is zero-padded half by half (each element
+keeps its rotation partner) and mixed dtypes compute in float32 (``_shape``).
 """
 
 from __future__ import annotations
@@ -29,6 +32,7 @@ from typing import Optional
 import torch
 
 from . import _lib
+from ._shape import compute_dtype, kernel_head_dim, pad_head_dim, pad_rope_halves, restore
 
 
 def _table(t: torch.Tensor, device) -> torch.Tensor:
@@ -149,13 +153,14 @@ def flash_attention_rope(
         kv_len = seq_len_k
     elif not 0 < kv_len <= seq_len_k:
         raise ValueError(f"kv_len must be in (0, {seq_len_k}], got {kv_len}")
-    if q.dtype != k.dtype or q.dtype != v.dtype:
-        raise ValueError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
     _lib.require_device(q, k, v)
     dev = q.device
-    return _RopeFn.apply(q.contiguous(), k.contiguous(), v.contiguous(), _table(q_cos, dev),
-                         _table(q_sin, dev), _table(k_cos, dev), _table(k_sin, dev),
-                         bool(causal), float(sm_scale), int(kv_len))
+    cdt, dp = compute_dtype(q, k, v), kernel_head_dim(head_dim)
+    tables = [pad_rope_halves(_table(t, dev), dp).contiguous() for t in (q_cos, q_sin, k_cos, k_sin)]
+    o = _RopeFn.apply(pad_rope_halves(q.to(cdt), dp).contiguous(), pad_rope_halves(k.to(cdt), dp).contiguous(),
+                      pad_head_dim(v.to(cdt), dp).contiguous(), *tables, bool(causal), float(sm_scale),
+                      int(kv_len))
+    return restore(o, head_dim, q.dtype)
 
 
 __all__ = ["flash_attention_rope"]

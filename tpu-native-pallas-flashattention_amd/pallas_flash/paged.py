@@ -23,6 +23,7 @@ from typing import Optional
 import torch
 
 from . import _lib
+from ._shape import adapt, compute_dtype, kernel_head_dim, restore
 
 
 def paged_flash_attention(
@@ -48,7 +49,8 @@ def paged_flash_attention(
         interpret: accepted for compatibility; ignored.
 
     Returns:
-        ``[batch, num_heads, 1, head_dim]`` in q's dtype.
+        ``[batch, num_heads, 1, head_dim]`` in q's dtype. head_dim other than
+        64/128 or mixed dtypes copy the pool padded/cast per call (``_shape``).
     """
     # paged.py:129-149
     if q.dim() != 4 or q.shape[2] != 1:
@@ -72,21 +74,21 @@ def paged_flash_attention(
             f"block_tables must be [batch, pages_per_seq], got {tuple(block_tables.shape)}")
     if tuple(context_lens.shape) != (batch,):
         raise ValueError(f"context_lens must be [batch], got {tuple(context_lens.shape)}")
-    if q.dtype != k_pages.dtype or q.dtype != v_pages.dtype:
-        raise ValueError("q and the page pools must share a dtype")
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
     _lib.require_device(q, k_pages, v_pages)
     dev = q.device
     tables = block_tables.to(device=dev, dtype=torch.int32).contiguous()
     lens = context_lens.to(device=dev, dtype=torch.int32).contiguous()
-    q, k_pages, v_pages = q.contiguous(), k_pages.contiguous(), v_pages.contiguous()
+    out_dtype = q.dtype
+    cdt, dp = compute_dtype(q, k_pages, v_pages), kernel_head_dim(head_dim)
+    q, k_pages, v_pages = (adapt(x, cdt, dp).contiguous() for x in (q, k_pages, v_pages))
     o = torch.empty_like(q)
     if batch == 0:
-        return o
+        return restore(o, head_dim, out_dtype)
     args = _lib.PagedArgs(
         _lib.ptr(q), _lib.ptr(k_pages), _lib.ptr(v_pages), _lib.ptr(tables), _lib.ptr(lens),
-        _lib.ptr(o), batch, num_heads, num_kv_heads, num_pages, page_size, head_dim,
+        _lib.ptr(o), batch, num_heads, num_kv_heads, num_pages, page_size, dp,
         tables.shape[1], float(sm_scale), _lib.dtype_tag(q), None, 0)
     L = _lib.lib()
     ws_bytes = L.pf_paged_attn_workspace_size(args)
@@ -95,7 +97,7 @@ def paged_flash_attention(
     args.workspace_bytes = ws.numel()
     with torch.cuda.device(dev):
         _lib.check(L.pf_paged_attn(args, _lib.stream_of(q)), "paged_flash_attention")
-    return o
+    return restore(o, head_dim, out_dtype)
 
 
 def init_paged_cache(num_pages: int, num_kv_heads: int, page_size: int, head_dim: int,
