@@ -361,20 +361,39 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     Frag pfr[PF];
     float mx = kNegInf;
     if constexpr (sizeof(T) == 2) {
-      // S_{j+1} MFMAs with the max update and exp/sum/pack of S_j beside
-      // them, then O^T += V_j^T P_j with the per-lane max of S_{j+1} beside it
-      // (slot = 32 / NV2 values).
+      // S_{j+1} MFMAs with the max update of S_j beside them, then
+      // O^T += V_j^T P_j with the exp/sum/pack of S_j and the per-lane max of
+      // S_{j+1} (32 / NV2 values per slot) beside it.
       constexpr int NV1 = G::CPR;
       constexpr int NV2 = 4 * NDT, VPS2 = 32 / NV2;
       // The row sum adds the float32 P (flash_attention.py:127-131: l from
       // the unrounded p; only the P.V operand is rounded).
       uint32_t pw[16];
       float rs = 0.f;
-      // Slots 0-1: finish the max of S_j (its per-lane part was taken beside
-      // the previous iteration's P.V MFMAs) and update m; slots 2.. : the 16
-      // exp pairs of S_j. The reduction thus runs beside MFMAs instead of
-      // between the last P.V MFMA and the barrier.
+      // Slots 0-1 of the S sequence: finish the max of S_j (its per-lane part
+      // was taken beside the previous iteration's P.V MFMAs) and update m.
+      // The 16 exp pairs of S_j: kSPairs beside the S MFMAs, the rest beside
+      // the P.V MFMAs: P.V MFMA k reads fragment k / NDT, so fragment f's four
+      // pairs run in slots [(f - 1) NDT, f NDT) and it is packed in the last
+      // of them, before its first MFMA. With the
+      // exp work out of the S sequence its MFMAs issue back to back while the
+      // max reduction and m update resolve: 4 of 16 pairs there measured
+      // 3.8% faster at config 3 than all 16 (same box, bit-identical: the
+      // row sum adds the pairs in the same order).
+      constexpr int kSPairs = 4;
+      static_assert(kSPairs >= 4 && kSPairs % 4 == 0 && kSPairs <= 16,
+                    "fragment 0 is packed before the P.V sequence; f >= 1 in slot (f - 1) NDT + (3 NDT) / 4 < f NDT");
       float mxr = kNegInf;
+      auto exp_pair = [&](int pr) __attribute__((always_inline)) {
+        const int v = 2 * pr;  // value v = tile v / 16, register v % 16
+        const float x0 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][v & 15], c2, -m_run));
+        const float x1 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][(v & 15) + 1], c2, -m_run));
+        pw[pr] = pack2<T>(x0, x1);
+        rs += x0 + x1;
+        // keeps the sum here: consumed only after the sequence, it would
+        // otherwise sink to the end and hold every exp result live
+        asm volatile("" : "+v"(rs));
+      };
       mfma_nat_il<T, D>(kcur, l32, hh, qf, s_nxt[0], s_nxt[1], [&](int i) {
         dma_part(i);
         if (i == 0) {
@@ -383,24 +402,23 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
           update_max(mxr);
         } else {
 #pragma unroll
-          for (int pr = ((i - 2) * 16) / (NV1 - 2); pr < ((i - 1) * 16) / (NV1 - 2); ++pr) {
-            const int v = 2 * pr;  // value v = tile v / 16, register v % 16
-            const float x0 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][v & 15], c2, -m_run));
-            const float x1 = __builtin_amdgcn_exp2f(fmaf(s_cur[v >> 4][(v & 15) + 1], c2, -m_run));
-            pw[pr] = pack2<T>(x0, x1);
-            rs += x0 + x1;
-            // keeps the sum here: consumed only after the sequence, it would
-            // otherwise sink to the end and hold every exp result live
-            asm volatile("" : "+v"(rs));
-          }
+          for (int pr = ((i - 2) * kSPairs) / (NV1 - 2); pr < ((i - 1) * kSPairs) / (NV1 - 2); ++pr) exp_pair(pr);
         }
       });
-      l_run += rs;
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int f = 0; f < kSPairs / 4; ++f)
         pfr[f] = __builtin_bit_cast(Frag, (u32x4){pw[4 * f], pw[4 * f + 1], pw[4 * f + 2], pw[4 * f + 3]});
       const int rel = lim - kv1 - 32 * hh;
       mfma_trn_il<T, D>(vcur, vta, pfr, acc, [&](int i) {
+#pragma unroll
+        for (int pr = kSPairs; pr < 16; ++pr) {
+          const int f = pr >> 2, q4 = pr & 3;
+          if (i == (f - 1) * NDT + (q4 * NDT) / 4) {
+            exp_pair(pr);
+            if (q4 == 3)
+              pfr[f] = __builtin_bit_cast(Frag, (u32x4){pw[4 * f], pw[4 * f + 1], pw[4 * f + 2], pw[4 * f + 3]});
+          }
+        }
 #pragma unroll
         for (int e = 0; e < VPS2; ++e) {
           const int v = i * VPS2 + e;
@@ -413,6 +431,7 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
         }
         asm volatile("" : "+v"(mx));  // keeps the max beside its MFMA (see rs)
       });
+      l_run += rs;
       mx_carry = mx;
     } else {
       mfma_nat<T, D>(kcur, l32, hh, qf, s_nxt[0], s_nxt[1]);
