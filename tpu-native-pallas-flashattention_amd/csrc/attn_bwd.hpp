@@ -1,7 +1,9 @@
-// Backward attention for gfx950: delta preprocess, dQ kernel, dK/dV kernel.
+// Backward attention for gfx950: dQ kernel (which also computes delta),
+// dK/dV kernel, and a standalone delta kernel for pf_attn_bwd_delta.
 //
 // Replaces `_flash_attention_bwd_call` (flash_attention.py:354-442):
-//   delta_i = sum_d o_id * do_id            (XLA op, :363-365) -> delta kernel
+//   delta_i = sum_d o_id * do_id            (XLA op, :363-365) -> in the dQ
+//                                            kernel (or the delta kernel)
 //   flash_attention_bwd_dq  pallas_call     (:379-398, kernel :276-311)
 //   flash_attention_bwd_dkv pallas_call     (:403-431, kernel :314-351)
 //   GQA group sum of per-head dK/dV         (:433-436)
