@@ -250,8 +250,11 @@ def bench_decode(L, _lib, torch, iters, warmup):
             {"q": q, "k": kc, "v": vc, "kv_len": kv_len})
 
 
-def bench_paged(L, _lib, torch, iters, warmup):
-    B, Hq, Hkv, D, page, npages, pps = 128, 32, 8, 128, 64, 16384, 128
+def cfg5_layout():
+    """Config 5's sequences and pool: lengths U[512, 8192] and the page
+    permutation from np.random.default_rng(0), pages dealt out in order, table
+    [128, 128] padded with -1; also the mask of pages some sequence uses."""
+    B, page, npages, pps = 128, 64, 16384, 128
     rng = np.random.default_rng(0)
     lens = rng.integers(512, 8193, B)
     perm = rng.permutation(npages)
@@ -263,6 +266,12 @@ def bench_paged(L, _lib, torch, iters, warmup):
         table[b, :n] = perm[cur:cur + n]
         used[perm[cur:cur + n]] = True
         cur += n
+    return lens, table, used
+
+
+def bench_paged(L, _lib, torch, iters, warmup):
+    B, Hq, Hkv, D, page, npages, pps = 128, 32, 8, 128, 64, 16384, 128
+    lens, table, used = cfg5_layout()
     g = torch.Generator(device="cuda").manual_seed(3)
     q = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
     kp = torch.randn((npages, Hkv, page, D), generator=g, device="cuda").to(torch.bfloat16)
@@ -295,6 +304,178 @@ def bench_paged(L, _lib, torch, iters, warmup):
     nbytes = int(lens.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2 + 4 * int(npg.sum()) + 4 * B
     del ws
     return ev.median_ms(0, 1), nbytes, {"q": q, "k": kp, "v": vp, "table": table, "lens": lens}
+
+
+def bench_aux(L, _lib, torch, iters, warmup):
+    """The rows around the hot path, each at a configuration's own shape:
+    the contiguous cache write (model.py _cache_write :257-262 as prefill and
+    decode steps call it; the ring slot scatter :447-448, :487) at config 4,
+    the paged page-write (paged.py:205-223, batched) into config 5's pool,
+    and the RoPE-aware VJP at config 2 (the inverse rotation pf_rope applies
+    to dQ and dK, and the whole RoPE training step beside the plain one).
+    Median ms per launch over back-to-back launches; bytes = rows read once
+    and written once (+ the tables for the rotation)."""
+    from pallas_flash import precompute_rope
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device="cuda").manual_seed(4)
+    mk = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+
+    def timed(fns):
+        for _ in range(max(3, warmup)):
+            for f in fns.values():
+                f()
+        ev = {k_: Events(2, iters) for k_ in fns}
+        for i in range(iters):
+            for k_, f in fns.items():
+                ev[k_].mark(i, 0)
+                f()
+                ev[k_].mark(i, 1)
+        torch.cuda.synchronize()
+        return {k_: e.median_ms(0, 1) for k_, e in ev.items()}
+
+    res, cpu_in = {}, {}
+    # contiguous cache at config 4's shape: a 6000-token prefill write, then
+    # a one-token ring step at position 15000 (slot 15000 % 8192 = 6808, past
+    # the prefill's slots)
+    B, Hkv, C, D, Lp = 64, 8, 8192, 128, 6000
+    kn, vn = mk(B, Hkv, Lp, D), mk(B, Hkv, Lp, D)
+    kc = torch.zeros((B, Hkv, C, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    pos0 = torch.zeros(B, dtype=torch.int32, device="cuda")
+    k1, v1 = mk(B, Hkv, 1, D), mk(B, Hkv, 1, D)
+    posr = torch.full((B,), 15000, dtype=torch.int32, device="cuda")
+    wa = _lib.KvWriteArgs(kn.data_ptr(), vn.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos0.data_ptr(), 1,
+                          B, Hkv, Lp, C, D, 0, 1)
+    wr = _lib.KvWriteArgs(k1.data_ptr(), v1.data_ptr(), kc.data_ptr(), vc.data_ptr(), posr.data_ptr(), 1,
+                          B, Hkv, 1, C, D, 1, 1)
+    t = timed({"prefill": lambda: ok(L.pf_kv_cache_write(wa, st), "pf_kv_cache_write"),
+               "ring": lambda: ok(L.pf_kv_cache_write(wr, st), "pf_kv_cache_write ring")})
+    assert torch.equal(kc[:, :, :Lp], kn) and torch.equal(vc[:, :, :Lp], vn), "cache write"
+    assert torch.equal(kc[:, :, 15000 % C], k1[:, :, 0]) and torch.equal(vc[:, :, 15000 % C], v1[:, :, 0])
+    res["kv_write_prefill"] = (t["prefill"], 2 * 2 * B * Hkv * Lp * D * 2)
+    res["kv_write_ring_step"] = (t["ring"], 2 * 2 * B * Hkv * D * 2)
+    cpu_in["kv"] = {"rows": kn[:8], "C": C}
+    del kn, vn, kc, vc, k1, v1
+
+    # paged: config 5's pool and table; a 512-token prefill chunk per
+    # sequence at position 0, then one token per sequence at its last
+    # position (lens - 1, always inside a mapped page)
+    lens, table, _ = cfg5_layout()
+    B5, npages, page, pps, Lc = 128, 16384, 64, 128, 512
+    kp = torch.zeros((npages, Hkv, page, D), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    tt = torch.as_tensor(table, device="cuda")
+    kn, vn = mk(B5, Hkv, Lc, D), mk(B5, Hkv, Lc, D)
+    k1, v1 = mk(B5, Hkv, 1, D), mk(B5, Hkv, 1, D)
+    p0 = torch.zeros(B5, dtype=torch.int32, device="cuda")
+    plast = torch.as_tensor((lens - 1).astype(np.int32), device="cuda")
+    pa = _lib.PagedWriteArgs(kn.data_ptr(), vn.data_ptr(), kp.data_ptr(), vp.data_ptr(), tt.data_ptr(),
+                             p0.data_ptr(), 1, B5, Hkv, Lc, npages, page, D, pps, 1)
+    ps = _lib.PagedWriteArgs(k1.data_ptr(), v1.data_ptr(), kp.data_ptr(), vp.data_ptr(), tt.data_ptr(),
+                             plast.data_ptr(), 1, B5, Hkv, 1, npages, page, D, pps, 1)
+    t = timed({"prefill": lambda: ok(L.pf_paged_cache_write(pa, st), "pf_paged_cache_write"),
+               "step": lambda: ok(L.pf_paged_cache_write(ps, st), "pf_paged_cache_write step")})
+    for b in (0, B5 - 1):
+        pg0 = int(table[b, 0])
+        assert torch.equal(kp[pg0], kn[b, :, :page]) and torch.equal(vp[pg0], vn[b, :, :page]), "paged write"
+        last = int(lens[b]) - 1
+        pgl = int(table[b, last // page])
+        assert torch.equal(kp[pgl, :, last % page], k1[b, :, 0]), "paged step write"
+    res["paged_write_prefill"] = (t["prefill"], 2 * 2 * B5 * Hkv * Lc * D * 2)
+    res["paged_write_step"] = (t["step"], 2 * 2 * B5 * Hkv * D * 2)
+    cpu_in["paged"] = {"rows": kn[:64], "page": page}
+    del kp, vp, kn, vn, k1, v1
+
+    # RoPE-aware VJP at config 2's shape
+    B2, Hq2, Hkv2, S2 = 4, 32, 8, 4096
+    cos, sin = precompute_rope(S2, D, 10000.0, device="cuda")
+    q, k, v, do = mk(B2, Hq2, S2, D), mk(B2, Hkv2, S2, D), mk(B2, Hkv2, S2, D), mk(B2, Hq2, S2, D)
+    buf = {n: torch.empty_like(t_) for n, t_ in (("qr", q), ("kr", k), ("o", q), ("dqr", q), ("dkr", k),
+                                                  ("dv", v), ("dq", q), ("dk", k))}
+    lse = torch.empty((B2, Hq2, S2), dtype=torch.float32, device="cuda")
+    delta = torch.empty_like(lse)
+    P = lambda t_: t_.data_ptr()
+    rope = lambda x, y, H, inv: _lib.RopeArgs(P(x), P(y), P(cos), P(sin), B2, H, S2, D, S2, inv, 1)
+    r_q, r_k = rope(q, buf["qr"], Hq2, 0), rope(k, buf["kr"], Hkv2, 0)
+    r_dq, r_dk = rope(buf["dqr"], buf["dq"], Hq2, 1), rope(buf["dkr"], buf["dk"], Hkv2, 1)
+    sc = 1.0 / D ** 0.5
+
+    def attn_args(qq, kk):
+        fa = _lib.FwdArgs(P(qq), P(kk), P(v), P(buf["o"]), P(lse), B2, Hq2, Hkv2, S2, S2, D, S2, 1, sc, 1)
+        ba = _lib.BwdArgs(P(qq), P(kk), P(v), P(buf["o"]), P(do), P(lse), P(delta), P(buf["dqr"]), P(buf["dkr"]),
+                          P(buf["dv"]), B2, Hq2, Hkv2, S2, S2, D, S2, 1, sc, 1)
+        return fa, ba
+
+    fa_r, ba_r = attn_args(buf["qr"], buf["kr"])
+    fa_p, ba_p = attn_args(q, k)
+
+    def rope_step():
+        ok(L.pf_rope(r_q, st), "pf_rope q")
+        ok(L.pf_rope(r_k, st), "pf_rope k")
+        ok(L.pf_attn_fwd(fa_r, st), "pf_attn_fwd")
+        ok(L.pf_attn_bwd(ba_r, st), "pf_attn_bwd")
+        ok(L.pf_rope(r_dq, st), "pf_rope dq (inverse)")
+        ok(L.pf_rope(r_dk, st), "pf_rope dk (inverse)")
+
+    def plain_step():
+        ok(L.pf_attn_fwd(fa_p, st), "pf_attn_fwd")
+        ok(L.pf_attn_bwd(ba_p, st), "pf_attn_bwd")
+
+    t = timed({"vjp": lambda: ok(L.pf_rope(r_dq, st), "pf_rope dq (inverse)"),
+               "rope_step": rope_step, "plain_step": plain_step})
+    res["rope_vjp"] = (t["vjp"], 2 * q.numel() * 2 + 2 * S2 * D * 4)
+    res["rope_train_step_ms"] = t["rope_step"]
+    res["plain_train_step_ms"] = t["plain_step"]
+    cpu_in["rope"] = {"g": buf["dqr"][0:1], "cos": cos, "sin": sin}
+    return res, cpu_in
+
+
+def cpu_baseline_aux(a):
+    """The aux rows on the CPU, each the oracle on a bounded sample: the
+    cache write (cache_write_ref, 2 of config 4's sequences, 6000 rows into a
+    zeroed 8192-slot cache, K only), the page write (paged_write_ref, 8 of
+    config 5's sequences, 512 rows each into a zeroed pool copy of 8192 pages)
+    and the inverse rotation (apply_rope_vjp_ref in float32, batch 0, 8 heads).
+    GB/s with the GPU's byte credit for the same rows (host copies untimed)."""
+    from oracle import apply_rope_vjp_ref, cache_write_ref, paged_write_ref
+    cores, blas = _host_cores()
+    out = {}
+    rows = a["kv"]["rows"].float().cpu().numpy()
+    B, H, Lp, D = rows.shape
+    cache = np.zeros((B, H, a["kv"]["C"], D), np.float32)
+    t0 = time.perf_counter()
+    cache_write_ref(cache, rows, 0)
+    dt = time.perf_counter() - t0
+    out["kv_write"] = {"value": 2 * B * H * Lp * D * 2 / dt / 1e9, "unit": "GB/s", "cores": cores,
+                       "blas_threads": blas, "kind": "port",
+                       "sample": f"numpy oracle (cache_write_ref) on {B} config-4 sequences x {H} kv heads, "
+                                 f"{Lp} rows at position 0 (K only), {dt:.2f} s"}
+    rows = a["paged"]["rows"].float().cpu().numpy()
+    B, H, Lc, D = rows.shape
+    page = a["paged"]["page"]
+    npg = Lc // page  # pages per sequence the rows fill
+    # a compact pool holding just the sample's pages (sequence b's page j at
+    # b * npg + j): the oracle copies the whole pool, whose size is not work
+    pool = np.zeros((B * npg, H, page, D), np.float32)
+    table = np.arange(B * npg, dtype=np.int32).reshape(B, npg)
+    t0 = time.perf_counter()
+    paged_write_ref(pool, rows, table, np.zeros(B, np.int64))
+    dt = time.perf_counter() - t0
+    out["paged_write"] = {"value": 2 * B * H * Lc * D * 2 / dt / 1e9, "unit": "GB/s", "cores": cores,
+                          "blas_threads": blas, "kind": "port",
+                          "sample": f"numpy oracle (paged_write_ref) on {B} config-5 sequences x {H} kv heads, "
+                                    f"{Lc} rows at position 0 into a pool of their {B * npg} pages (K only), "
+                                    f"{dt:.2f} s"}
+    gq = a["rope"]["g"].float().cpu().numpy()
+    cos, sin = a["rope"]["cos"].cpu().numpy(), a["rope"]["sin"].cpu().numpy()
+    t0 = time.perf_counter()
+    apply_rope_vjp_ref(gq, cos, sin, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    out["rope_vjp"] = {"value": 2 * gq.size * 2 / dt / 1e9, "unit": "GB/s", "cores": cores,
+                       "blas_threads": blas, "kind": "port",
+                       "sample": f"numpy float32 oracle (apply_rope_vjp_ref) on config 2's dQ, batch 0, "
+                                 f"{gq.shape[1]} of 32 heads, {dt:.2f} s"}
+    return out
 
 
 def bench_read_ceiling(torch, iters):
@@ -493,7 +674,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "stream", "copy"],
+    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "aux", "stream", "copy"],
                     default="all")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
@@ -552,6 +733,24 @@ def main():
             log("cpu baseline cfg5 ...")
             cpu_sec["paged"] = cpu_baseline_paged(pin)
         del pin
+
+    if args.only in ("all", "aux"):
+        log("cache writes and RoPE VJP ...")
+        res, ain = bench_aux(L, _lib, torch, iters, args.warmup)
+        for k_ in ("kv_write_prefill", "paged_write_prefill", "rope_vjp"):
+            ms, nb = res[k_]
+            sec[f"{k_}_gbs"] = nb / (ms * 1e-3) / 1e9
+            sec[f"{k_}_ms"] = ms
+            sec[f"{k_}_frac_hbm"] = sec[f"{k_}_gbs"] / PEAK_HBM_GBS
+        for k_ in ("kv_write_ring_step", "paged_write_step"):
+            sec[f"{k_}_us"] = res[k_][0] * 1e3
+        sec["rope_train_step_ms"] = res["rope_train_step_ms"]
+        sec["plain_train_step_cfg2_shape_ms"] = res["plain_train_step_ms"]
+        sec["rope_train_over_plain"] = res["rope_train_step_ms"] / res["plain_train_step_ms"]
+        if not args.skip_cpu:
+            log("cpu baselines aux ...")
+            cpu_sec.update(cpu_baseline_aux(ain))
+        del ain
 
     if args.only in ("all", "stream"):
         log("hbm read ceiling ...")
