@@ -39,3 +39,33 @@ def test_more_than_one_gpu_is_refused():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_cfg5_layout_matches_the_stated_workload():
+    """Config 5 as the measurement contract states it: lengths from
+    default_rng(0) in [512, 8192] summing to 567,626 tokens, pages dealt out
+    of one permutation (no page shared), the table -1-padded past each
+    sequence's ceil(len / 64) pages."""
+    import numpy as np
+    lens, table, used = bench.cfg5_layout()
+    assert lens.shape == (128,) and lens.min() >= 512 and lens.max() <= 8192
+    assert int(lens.sum()) == 567_626
+    npg = -(-lens // 64)
+    for b in range(128):
+        assert (table[b, :npg[b]] >= 0).all() and (table[b, npg[b]:] == -1).all()
+    mapped = table[table >= 0]
+    assert len(np.unique(mapped)) == mapped.size == int(npg.sum()) == int(used.sum())
+
+
+def test_aux_cpu_baselines_run_on_small_inputs():
+    import torch
+    g = torch.Generator().manual_seed(0)
+    mk = lambda *s: torch.randn(s, generator=g).to(torch.bfloat16)
+    cos = torch.rand(16, 64)
+    sin = torch.rand(16, 64)
+    a = {"kv": {"rows": mk(2, 2, 12, 64), "C": 32}, "paged": {"rows": mk(3, 2, 8, 64), "page": 4},
+         "rope": {"g": mk(1, 2, 16, 64), "cos": cos, "sin": sin}}
+    out = bench.cpu_baseline_aux(a)
+    assert set(out) == {"kv_write", "paged_write", "rope_vjp"}
+    for v in out.values():
+        assert v["unit"] == "GB/s" and v["value"] > 0 and v["kind"] == "port" and v["cores"] >= 1
