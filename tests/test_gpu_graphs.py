@@ -1,4 +1,5 @@
-"""GPU tier: the prefill training step and paged decode captured in HIP graphs
+"""GPU tier: the prefill training step, paged decode, fused RoPE and decode
+captured in HIP graphs
 (torch.cuda.graph over the C-ABI launches) and replayed.
 
 Every launch of these paths runs on torch's current stream, allocates only
@@ -85,3 +86,35 @@ def test_paged_decode_graph_replay_lengths_on_device():
         assert torch.equal(o_g, o_e), f"replay {it}"
         lens.add_(5).clamp_(max=pps * page)
         q.copy_(torch.randn(q.shape, generator=g, device=DEV).to(q.dtype))
+
+
+def test_rope_forward_and_decode_graph_replay():
+    """The fused-RoPE forward (its rotated-K workspace from the graph pool)
+    and the contiguous decode captured together; replays with new inputs
+    equal the eager calls."""
+    from pallas_flash import flash_attention_decode, flash_attention_rope, precompute_rope
+    note("graph: rope forward + decode")
+    g = torch.Generator(device=DEV).manual_seed(23)
+    mk = lambda *s: torch.randn(s, generator=g, device=DEV).to(torch.bfloat16)
+    B, Hq, Hkv, S, D = 2, 8, 2, 320, 128
+    cos, sin = precompute_rope(S, D, 10000.0, device=DEV)
+    q, k, v = mk(B, Hq, S, D), mk(B, Hkv, S, D), mk(B, Hkv, S, D)
+    qd, kc, vc = mk(4, 8, 1, D), mk(4, 2, 512, D), mk(4, 2, 512, D)
+
+    def run():
+        with torch.no_grad():
+            return (flash_attention_rope(q, k, v, cos, sin, causal=True),
+                    flash_attention_decode(qd, kc, vc, 300))
+
+    _warm(run)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs_g = run()
+    for it in range(4):
+        for t in (q, k, v, qd, kc):
+            t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(t.dtype))
+        graph.replay()
+        outs_e = run()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("rope", "decode"), outs_g, outs_e):
+            assert torch.equal(a, b), f"replay {it}: {name}"
