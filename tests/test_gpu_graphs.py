@@ -1,6 +1,6 @@
 """GPU tier: the prefill training step, paged decode, fused RoPE and decode
-captured in HIP graphs
-(torch.cuda.graph over the C-ABI launches) and replayed.
+captured in HIP graphs (torch.cuda.graph over the C-ABI launches) and
+replayed.
 
 Every launch of these paths runs on torch's current stream, allocates only
 through torch (graph-private pool under capture), issues no memset and reads
