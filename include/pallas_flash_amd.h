@@ -59,10 +59,13 @@ typedef enum { PF_DTYPE_F32 = 0, PF_DTYPE_BF16 = 1, PF_DTYPE_F16 = 2 } pf_dtype;
  *       lse = 0.
  *   kv_len in (0, seq_len_k]; keys >= kv_len are never read.
  *   causal: q_pos >= k_pos, top-left aligned (also when seq_len_q != seq_len_k).
- * Tuning: fwd_rows_per_wave = 64 (pf_set_tuning, or PF_FWD_ROWS_PER_WAVE=64
- * in the environment at the first call) selects the 64-rows-per-wave kernel
- * for bf16/f16 with head_dim 128 (same results, one workgroup per CU); the
- * default 32 keeps the 32-row kernel. Also applies to pf_attn_fwd_rope.
+ * Work distribution: the kernel's work items (a query block of up to four
+ * query heads of one GQA group) are placed on the GPU's XCDs in an L2-aware
+ * order; with pf_tuning.tail_dynamic_pct > 0 and at least 1024 items, that
+ * share of the items (the lightest) is instead handed out at run time to
+ * whichever XCD is free, through a per-stream counter in a static device
+ * array (no allocation; a launch recorded into a graph gets its own counter).
+ * Results are bit-identical either way. Also applies to pf_attn_fwd_rope.
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* q;
@@ -376,9 +379,9 @@ int pf_attn_decode_step(const pf_attn_decode_step_args* args, void* stream);
  * arguments of its pallas_calls (flash_attention.py:479-490), which this
  * build accepts and ignores. Initial values come from the environment, read
  * once per process at the first launch or tuning call:
- *   PF_FWD_ROWS_PER_WAVE  32 (default) or 64: query rows per wave of the
- *                         16-bit head_dim-128 forward (64: one workgroup per
- *                         CU, half the LDS reads per matrix-core op)
+ *   PF_TAIL_DYNAMIC_PCT    0 .. 100: percentage of the forward's work items
+ *                         handed out at run time to whichever XCD is free
+ *                         (0: every item placed statically)
  *   PF_DECODE_STAGES      2 (default) .. 4: LDS ring depth of the streaming
  *                         decode / paged kernel
  *   PF_DECODE_WAVES       0 (default: one per resident slot, queried once per
@@ -388,7 +391,7 @@ int pf_attn_decode_step(const pf_attn_decode_step_args* args, void* stream);
  * call from any thread.
  * ------------------------------------------------------------------------- */
 typedef struct {
-  int32_t fwd_rows_per_wave;
+  int32_t tail_dynamic_pct;
   int32_t decode_stages;
   int32_t decode_waves;
 } pf_tuning;

@@ -223,8 +223,8 @@ static void test_tuning_and_version() {
   EXPECT(pf_set_tuning(NULL) == PF_ERR_INVALID, "set_tuning NULL");
   EXPECT(pf_get_tuning(&t) == PF_OK, "get_tuning");
   u = t;
-  u.fwd_rows_per_wave = 48;
-  EXPECT(pf_set_tuning(&u) == PF_ERR_INVALID, "set_tuning rows");
+  u.tail_dynamic_pct = 101;
+  EXPECT(pf_set_tuning(&u) == PF_ERR_INVALID, "set_tuning dynamic share");
   u = t;
   u.decode_stages = 5;
   EXPECT(pf_set_tuning(&u) == PF_ERR_INVALID, "set_tuning stages");

@@ -271,24 +271,28 @@ def test_rope_rejects_on_host(L, over, status):
     assert L.pf_rope(_rope_args(**over), None) == status
 
 
+# pf_tuning defaults (capi.hip: Tuning)
+TUNING_DEFAULTS = {"tail_dynamic_pct": 30, "decode_stages": 2, "decode_waves": 0}
+
+
 def test_tuning_round_trip_and_rejections(L):
     """pf_get_tuning / pf_set_tuning: defaults (no PF_* variables in this
     environment), out-of-range values refused without changing anything,
     and the context manager restores the previous values."""
     import os
-    if any(v in os.environ for v in ("PF_FWD_ROWS_PER_WAVE", "PF_DECODE_STAGES", "PF_DECODE_WAVES")):
+    if any(v in os.environ for v in ("PF_TAIL_DYNAMIC_PCT", "PF_DECODE_STAGES", "PF_DECODE_WAVES")):
         pytest.skip("tuning variables set in this environment")
-    assert _lib.get_tuning() == {"fwd_rows_per_wave": 32, "decode_stages": 2, "decode_waves": 0}
-    for bad in (dict(fwd_rows_per_wave=48), dict(decode_stages=1), dict(decode_stages=5),
-                dict(decode_waves=-1)):
+    assert _lib.get_tuning() == TUNING_DEFAULTS
+    for bad in (dict(tail_dynamic_pct=-1), dict(tail_dynamic_pct=101), dict(decode_stages=1),
+                dict(decode_stages=5), dict(decode_waves=-1)):
         t = _lib.Tuning(**{**_lib.get_tuning(), **bad})
         assert L.pf_set_tuning(ctypes.byref(t)) == _lib.PF_ERR_INVALID
-        assert _lib.get_tuning()["fwd_rows_per_wave"] == 32
+        assert _lib.get_tuning() == TUNING_DEFAULTS
     assert L.pf_set_tuning(None) == _lib.PF_ERR_INVALID
     assert L.pf_get_tuning(None) == _lib.PF_ERR_INVALID
-    with _lib.tuning(fwd_rows_per_wave=64, decode_waves=7) as t:
-        assert t == _lib.get_tuning() == {"fwd_rows_per_wave": 64, "decode_stages": 2, "decode_waves": 7}
-    assert _lib.get_tuning() == {"fwd_rows_per_wave": 32, "decode_stages": 2, "decode_waves": 0}
+    with _lib.tuning(tail_dynamic_pct=37, decode_waves=7) as t:
+        assert t == _lib.get_tuning() == {**TUNING_DEFAULTS, "tail_dynamic_pct": 37, "decode_waves": 7}
+    assert _lib.get_tuning() == TUNING_DEFAULTS
     with pytest.raises(TypeError):
         with _lib.tuning(block_q=64):
             pass

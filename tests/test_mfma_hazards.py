@@ -1,7 +1,6 @@
 """CPU tier: wait states after the inline-assembly MFMAs.
 
-The dK/dV kernel (MfmaAgpr) and the 64-row forward (MfmaVA, MfmaAgpr) issue
-32x32x16 MFMAs from inline assembly. The compiler's hazard recognizer cannot
+The dK/dV kernel (MfmaAgpr) issues 32x32x16 MFMAs from inline assembly. The compiler's hazard recognizer cannot
 see inside the asm, so it adds no wait states before its own reads of the
 results -- including register copies it inserts on its own. The kernels
 route every such result through a tied s_nop fence; this test compiles the
@@ -28,7 +27,6 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 NEED = 12
 
 SOURCES = {
-    "attn_fwd_w64.hip": [],
     "attn_bwd_dkv16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
@@ -107,7 +105,7 @@ def test_inline_asm_mfma_results_are_fenced():
         for name, body in _kernels(asm).items():
             n_kernels += 1
             problems += [f"{src} {name[:60]}: {p}" for p in scan(body)]
-    assert n_kernels >= 8, f"expected the MFMA kernels of {list(SOURCES)}, found {n_kernels}"
+    assert n_kernels >= 4, f"expected the MFMA kernels of {list(SOURCES)}, found {n_kernels}"
     assert not problems, "\n".join(problems[:20])
 
 

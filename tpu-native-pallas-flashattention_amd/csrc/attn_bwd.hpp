@@ -80,7 +80,9 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   __shared__ __attribute__((aligned(16))) char smem[4 * G::BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
-  const int w = xcd_remap(blockIdx.x, n_work, p.g);
+  const int item = work_tail_item(p.tail, n_work, reinterpret_cast<int*>(smem));
+  if (item < 0) return;
+  const int w = xcd_remap(item, n_work, p.g);
   const int member = w % p.g;
   int rest = w / p.g;
   const int kvh = rest % p.Hkv;
@@ -330,7 +332,8 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
   // heavy first: for causal, early key blocks are attended by the most queries
-  const int w = blockIdx.x;
+  const int w = work_tail_item(p.tail, n_kblk * p.B * p.Hkv, reinterpret_cast<int*>(smem));
+  if (w < 0) return;
   const int kblk = w / (p.B * p.Hkv);
   const int bk = w % (p.B * p.Hkv);
   const int b = bk / p.Hkv, kvh = bk % p.Hkv;
@@ -741,22 +744,23 @@ hipError_t delta_typed(const BwdParams& p, hipStream_t st) {
 template <typename T, int D>
 hipError_t dq_typed(const BwdParams& p, bool causal, hipStream_t st) {
   const int n_qblk = (p.Sq + 127) / 128;
-  const int n_work = p.B * p.Hq * n_qblk;
+  const int n_work = bwd_dq_items(p);
+  const dim3 grid(work_tail_grid(p.tail, n_work));
   if (causal)
-    hipLaunchKernelGGL((pf_attn_bwd_dq_kernel<T, D, true>), dim3(n_work), dim3(256), 0, st, p, n_qblk, n_work);
+    hipLaunchKernelGGL((pf_attn_bwd_dq_kernel<T, D, true>), grid, dim3(256), 0, st, p, n_qblk, n_work);
   else
-    hipLaunchKernelGGL((pf_attn_bwd_dq_kernel<T, D, false>), dim3(n_work), dim3(256), 0, st, p, n_qblk, n_work);
+    hipLaunchKernelGGL((pf_attn_bwd_dq_kernel<T, D, false>), grid, dim3(256), 0, st, p, n_qblk, n_work);
   return hipGetLastError();
 }
 
 template <typename T, int D>
 hipError_t dkv_typed(const BwdParams& p, bool causal, hipStream_t st) {
   const int n_kblk = (p.Sk + 127) / 128;
-  const int n_work = p.B * p.Hkv * n_kblk;
+  const dim3 grid(work_tail_grid(p.tail, bwd_dkv_items(p)));
   if (causal)
-    hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, true>), dim3(n_work), dim3(256), 0, st, p, n_kblk);
+    hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, true>), grid, dim3(256), 0, st, p, n_kblk);
   else
-    hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, false>), dim3(n_work), dim3(256), 0, st, p, n_kblk);
+    hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, false>), grid, dim3(256), 0, st, p, n_kblk);
   return hipGetLastError();
 }
 

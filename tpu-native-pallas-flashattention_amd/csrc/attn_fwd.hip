@@ -88,7 +88,9 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   // work item = (batch, kv head, head group, query block); the workgroup's
   // waves split into hpw heads x (4 / hpw) 32-row slices.
   int b, kvh, hg, qblk;
-  fwd_work_item(blockIdx.x, p, b, kvh, hg, qblk);
+  const int item = work_tail_item(p.tail, p.n_work, reinterpret_cast<int*>(smem));
+  if (item < 0) return;
+  fwd_work_item(item, p, b, kvh, hg, qblk);
   const int wph = 4 / p.hpw;  // waves per head
   const int h = kvh * p.g + hg * p.hpw + wv / wph;
 
@@ -573,7 +575,7 @@ __global__ __launch_bounds__(256) void pf_rope_rotate_k_kernel(const T* __restri
 
 template <typename T, int D>
 hipError_t launch_typed(const FwdParams& p, bool causal, bool rope, hipStream_t st) {
-  const dim3 grid(p.n_work), block(256);
+  const dim3 grid(work_tail_grid(p.tail, p.n_work)), block(256);
   if (causal) {
     if (rope) hipLaunchKernelGGL((pf_attn_fwd_kernel<T, D, true, true>), grid, block, 0, st, p);
     else hipLaunchKernelGGL((pf_attn_fwd_kernel<T, D, true, false>), grid, block, 0, st, p);
@@ -628,11 +630,6 @@ hipError_t launch_rope_rotate_k(const void* k, void* k_out, const float* cos, co
 
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream) {
-  if (p.rows_per_wave == 64) {
-    if (head_dim != 128) return hipErrorInvalidValue;
-    return launch_attn_fwd_w64(p, dtype, causal, rope, stream);
-  }
-  if (p.rows_per_wave != 32) return hipErrorInvalidValue;
   switch (dtype) {
     case kF32: return launch_dim<float>(p, head_dim, causal, rope, stream);
     case kBF16: return launch_dim<bf16_t>(p, head_dim, causal, rope, stream);

@@ -16,24 +16,27 @@ namespace {
 // Process-wide tuning (pf_get_tuning / pf_set_tuning). The environment is read
 // once, at the first call that needs a value; afterwards every launch reads
 // three atomics and makes no environment or device query of its own.
+// Share of a prefill launch's work items handed out by tickets (plan_tail).
+constexpr int kDefaultTailDynamicPct = 30;
+
 struct Tuning {
-  std::atomic<int> fwd_rows_per_wave{32};
+  std::atomic<int> tail_dynamic_pct{kDefaultTailDynamicPct};
   std::atomic<int> decode_stages{2};
   std::atomic<int> decode_waves{0};
 };
 
-bool tuning_valid(int rows, int stages, int waves) {
-  return (rows == 32 || rows == 64) && stages >= 2 && stages <= 4 && waves >= 0;
+bool tuning_valid(int dyn, int stages, int waves) {
+  return dyn >= 0 && dyn <= 100 && stages >= 2 && stages <= 4 && waves >= 0;
 }
 
 Tuning& tuning() {
   static Tuning t;
   static std::once_flag once;
   std::call_once(once, [] {
-    const char* r = getenv("PF_FWD_ROWS_PER_WAVE");
+    const char* f = getenv("PF_TAIL_DYNAMIC_PCT");
     const char* s = getenv("PF_DECODE_STAGES");
     const char* w = getenv("PF_DECODE_WAVES");
-    if (r != nullptr && atoi(r) == 64) t.fwd_rows_per_wave = 64;
+    if (f != nullptr && atoi(f) >= 0 && atoi(f) <= 100) t.tail_dynamic_pct = atoi(f);
     if (s != nullptr && atoi(s) >= 2 && atoi(s) <= 4) t.decode_stages = atoi(s);
     if (w != nullptr && atoi(w) > 0) t.decode_waves = atoi(w);
   });
@@ -58,17 +61,6 @@ int check_attn_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, 
 }
 
 int finish(hipError_t e) { return e == hipSuccess ? PF_OK : PF_ERR_LAUNCH; }
-
-// Query rows per wave of the forward kernel: 32 (attn_fwd.hip). The 64-row
-// tiling (attn_fwd_w64.hip: bf16/f16, D = 128, one wave per SIMD) is opt-in
-// through the tuning (fwd_rows_per_wave = 64): it halves the LDS reads per
-// MFMA but measures slower at the headline shapes (every barrier and every
-// work item's prologue and epilogue is exposed at one workgroup per CU).
-int fwd_rows_per_wave(const pf_attn_fwd_args* a) {
-  const bool wide_ok = a->dtype != PF_DTYPE_F32 && a->head_dim == 128;
-  if (!wide_ok) return 32;
-  return tuning().fwd_rows_per_wave.load(std::memory_order_relaxed) == 64 ? 64 : 32;
-}
 
 // (batch, kv head) pairs each XCD streams at a time in the forward
 // (fwd_work_item): with more than one pair per XCD, the largest divisor of
@@ -111,8 +103,7 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   // A workgroup's 4 waves cover hpw query heads of one GQA group x rpw rows:
   // the K/V tiles it stages serve all of them.
   p->hpw = (p->g % 4 == 0) ? 4 : (p->g % 2 == 0) ? 2 : 1;
-  p->rows_per_wave = fwd_rows_per_wave(a);
-  p->rpw = 4 * p->rows_per_wave / p->hpw;
+  p->rpw = 128 / p->hpw;
   p->n_qblk = (a->seq_len_q + p->rpw - 1) / p->rpw;
   const int64_t n_work = (int64_t)a->batch * (a->num_heads / p->hpw) * p->n_qblk;
   if (n_work > kMaxGrid) return PF_ERR_UNSUPPORTED;
@@ -120,8 +111,39 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
   if ((int64_t)(a->seq_len_k + 256) * a->head_dim * 4 > 0x7fffffff) return PF_ERR_UNSUPPORTED;
   p->n_work = (int)n_work;
   p->pair_group = fwd_pair_group(a);
+  p->tail = pf::WorkTail{nullptr, p->n_work, 0};
   return PF_OK;
 }
+
+// Dynamic tail of a prefill launch (pf::WorkTail): the last tail_dynamic_pct
+// percent of the work items (the lightest under the heavy-first orders) go to
+// ticket-drawing workgroups, kTailSlack times as many as those items so an
+// XCD that runs ahead can take up to that multiple of its share. The static
+// part is a multiple of the 8 XCDs so each gets the same number of its own
+// items. Launches of fewer than min_items items (two per resident workgroup
+// slot of the kernel) keep every item static, as do launches whose stream
+// gets no ticket counter.
+constexpr double kTailSlack = 2.0;
+
+pf::WorkTail plan_tail(int n_work, int min_items, hipStream_t stream) {
+  pf::WorkTail w{nullptr, n_work, 0};
+  const int pct = tuning().tail_dynamic_pct.load(std::memory_order_relaxed);
+  if (pct <= 0 || n_work < min_items) return w;
+  const int n_static = 8 * (int)(((int64_t)n_work * (100 - pct) / 100) / 8);
+  const int pool = n_work - n_static;
+  if (pool <= 0) return w;
+  unsigned int* t = pf::work_tickets(stream);
+  if (t == nullptr) return w;
+  w.tickets = t;
+  w.n_static = n_static;
+  w.n_tickets = (int)(pool * kTailSlack) + 1;
+  return w;
+}
+
+// Minimum items for a dynamic tail: two per resident workgroup slot of a
+// 256-CU MI355X (the 16-bit forward and dQ run two workgroups per CU, dK/dV
+// one).
+constexpr int kTwoPerCu = 2 * 2 * 256, kOnePerCu = 2 * 256;
 
 }  // namespace
 
@@ -132,17 +154,17 @@ const char* pf_version(void) { return "pallas_flash_amd 0.1.0 (gfx950)"; }
 int pf_get_tuning(pf_tuning* out) {
   if (!out) return PF_ERR_INVALID;
   Tuning& t = tuning();
-  out->fwd_rows_per_wave = t.fwd_rows_per_wave.load();
+  out->tail_dynamic_pct = t.tail_dynamic_pct.load();
   out->decode_stages = t.decode_stages.load();
   out->decode_waves = t.decode_waves.load();
   return PF_OK;
 }
 
 int pf_set_tuning(const pf_tuning* in) {
-  if (!in || !tuning_valid(in->fwd_rows_per_wave, in->decode_stages, in->decode_waves))
+  if (!in || !tuning_valid(in->tail_dynamic_pct, in->decode_stages, in->decode_waves))
     return PF_ERR_INVALID;
   Tuning& t = tuning();
-  t.fwd_rows_per_wave = in->fwd_rows_per_wave;
+  t.tail_dynamic_pct = in->tail_dynamic_pct;
   t.decode_stages = in->decode_stages;
   t.decode_waves = in->decode_waves;
   return PF_OK;
@@ -154,6 +176,7 @@ int pf_attn_fwd(const pf_attn_fwd_args* a, void* stream) {
   int st = fill_fwd(a, &p);
   if (st != PF_OK) return st;
   if (p.n_work == 0) return PF_OK;
+  p.tail = plan_tail(p.n_work, kTwoPerCu, (hipStream_t)stream);
   return finish(pf::launch_attn_fwd(p, a->dtype, a->head_dim, a->causal != 0, false,
                                     (hipStream_t)stream));
 }
@@ -190,6 +213,7 @@ int pf_attn_fwd_rope(const pf_attn_fwd_rope_args* a, void* stream) {
   p.q_cos = a->q_cos;
   p.q_sin = a->q_sin;
   p.lse = nullptr;  // the reference's fused kernel has no LSE output
+  p.tail = plan_tail(p.n_work, kTwoPerCu, s);
   return finish(pf::launch_attn_fwd(p, a->base.dtype, a->base.head_dim, a->base.causal != 0, true, s));
 }
 
@@ -223,6 +247,7 @@ static int fill_bwd(const pf_attn_bwd_args* a, pf::BwdParams* p, bool need_grads
   p->g = a->num_heads / a->num_kv_heads;
   p->sm_scale = a->sm_scale;
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p->tail = pf::WorkTail{nullptr, 0, 0};
   const int64_t rows = (int64_t)a->batch * a->num_heads * a->seq_len_q;
   if (rows > kMaxGrid) return PF_ERR_UNSUPPORTED;
   // Per-(batch, head) byte offsets and buffer sizes are 32-bit inside the
@@ -246,6 +271,7 @@ int pf_attn_bwd_dq(const pf_attn_bwd_args* a, void* stream) {
   int st = fill_bwd(a, &p, true);
   if (st != PF_OK) return st;
   if ((int64_t)p.B * p.Hq * p.Sq == 0) return PF_OK;
+  p.tail = plan_tail(pf::bwd_dq_items(p), kTwoPerCu, (hipStream_t)stream);
   return finish(pf::launch_attn_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, (hipStream_t)stream));
 }
 
@@ -254,6 +280,7 @@ int pf_attn_bwd_dkv(const pf_attn_bwd_args* a, void* stream) {
   int st = fill_bwd(a, &p, true);
   if (st != PF_OK) return st;
   if ((int64_t)p.B * p.Hkv * p.Sk == 0) return PF_OK;
+  p.tail = plan_tail(pf::bwd_dkv_items(p), kOnePerCu, (hipStream_t)stream);
   return finish(pf::launch_attn_bwd_dkv(p, a->dtype, a->head_dim, a->causal != 0, (hipStream_t)stream));
 }
 
@@ -264,11 +291,14 @@ int pf_attn_bwd(const pf_attn_bwd_args* a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if ((int64_t)p.B * p.Hq * p.Sq > 0) {
     // the dQ kernel computes delta itself and stores it for dK/dV
+    p.tail = plan_tail(pf::bwd_dq_items(p), kTwoPerCu, s);
     st = finish(pf::launch_attn_bwd_dq(p, a->dtype, a->head_dim, a->causal != 0, s));
     if (st != PF_OK) return st;
   }
-  if ((int64_t)p.B * p.Hkv * p.Sk > 0)
+  if ((int64_t)p.B * p.Hkv * p.Sk > 0) {
+    p.tail = plan_tail(pf::bwd_dkv_items(p), kOnePerCu, s);
     st = finish(pf::launch_attn_bwd_dkv(p, a->dtype, a->head_dim, a->causal != 0, s));
+  }
   return st;
 }
 

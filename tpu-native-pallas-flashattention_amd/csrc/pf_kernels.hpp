@@ -10,6 +10,50 @@
 
 namespace pf {
 
+// Dynamic tail of a prefill launch (forward, dQ, dK/dV). Workgroups are
+// dispatched round-robin over the 8 XCDs, and each XCD starts its workgroups
+// in blockIdx order as its CUs free up; XCDs run at somewhat different
+// speeds, so with a fixed item per workgroup they finish apart (up to 5-8%
+// of a launch). Workgroups [0, n_static) take work item blockIdx (each XCD's
+// share, with the L2 locality the item order gives it); each of the
+// n_tickets workgroups after them draws a ticket t from *tickets and takes
+// item n_static + t (none when t >= n_work - n_static), so an XCD that runs
+// ahead takes more of the remaining, lightest items. tickets null: every
+// item static (grid = n_work).
+struct WorkTail {
+  unsigned int* tickets;
+  int n_static;
+  int n_tickets;
+};
+
+// The ticket counter of a dynamic-tail launch on `stream` (zero between
+// launches; work_tickets.hip), or null: launch without a dynamic tail.
+unsigned int* work_tickets(hipStream_t stream);
+
+__host__ __device__ inline int work_tail_grid(const WorkTail& t, int n_work) {
+  return t.tickets ? t.n_static + t.n_tickets : n_work;
+}
+
+// Work-item index of the calling workgroup (WorkTail). The workgroup that
+// draws the last ticket sets the counter back to zero for the next launch on
+// the stream. Returns -1 for a workgroup that finds no item left (it exits).
+// Uniform over the workgroup. `lds` is any LDS word of the workgroup: a
+// drawing workgroup passes the ticket through it between two barriers, so it
+// is free again on return.
+__device__ inline int work_tail_item(const WorkTail& w, int n_work, int* lds) {
+  const int bid = blockIdx.x;
+  if (w.tickets == nullptr || bid < w.n_static) return bid;
+  if (threadIdx.x == 0) {
+    const unsigned t = __hip_atomic_fetch_add(w.tickets, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == (unsigned)w.n_tickets - 1u) __hip_atomic_store(w.tickets, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds = (int)t;
+  }
+  __syncthreads();
+  const int t = *lds;
+  __syncthreads();  // every wave has read the word before any reuses it
+  return t < n_work - w.n_static ? w.n_static + t : -1;
+}
+
 // Forward prefill (optionally with fused RoPE).
 struct FwdParams {
   const void* q;
@@ -21,12 +65,12 @@ struct FwdParams {
   const float* q_sin;
   int B, Hq, Hkv, Sq, Sk, kv_len, g;
   float scale_log2;  // sm_scale * log2(e)
-  int rows_per_wave; // 32 (attn_fwd.hip) or 64 (attn_fwd_w64.hip: 16-bit, D = 128)
   int hpw;           // query heads per workgroup (1, 2 or 4; divides g)
-  int rpw;           // query rows per head per workgroup (4 * rows_per_wave / hpw)
+  int rpw;           // query rows per head per workgroup (128 / hpw: 32 per wave)
   int n_qblk;        // ceil(Sq / rpw)
   int n_work;        // B * Hq / hpw * n_qblk
   int pair_group;    // > 0: (batch, kv head) pairs an XCD streams at a time (fwd_work_item)
+  WorkTail tail;
 };
 
 // Work item of forward workgroup `bid`: (batch b, kv head kvh, head group hg
@@ -66,8 +110,6 @@ __device__ inline void fwd_work_item(int bid, const FwdParams& p, int& b, int& k
 
 hipError_t launch_attn_fwd(const FwdParams& p, int dtype, int head_dim, bool causal, bool rope,
                            hipStream_t stream);
-// The 64-rows-per-wave forward (p.rows_per_wave == 64; bf16/f16, D = 128).
-hipError_t launch_attn_fwd_w64(const FwdParams& p, int dtype, bool causal, bool rope, hipStream_t stream);
 
 // Rotate rows [0, kv_len) of every (batch, head) of a [B, H, Sk, D] tensor
 // into k_out (same layout): x*cos + rotate_half(x)*sin with the [>= kv_len, D]
@@ -91,7 +133,13 @@ struct BwdParams {
   int B, Hq, Hkv, Sq, Sk, kv_len, g;
   float sm_scale;
   float scale_log2;
+  WorkTail tail;  // of the kernel being launched (dQ or dK/dV)
 };
+
+// Work items of the dQ kernel (128 query rows of one head) and of the dK/dV
+// kernel (128 keys of one kv head, all its query heads).
+inline int bwd_dq_items(const BwdParams& p) { return p.B * p.Hq * ((p.Sq + 127) / 128); }
+inline int bwd_dkv_items(const BwdParams& p) { return p.B * p.Hkv * ((p.Sk + 127) / 128); }
 
 hipError_t launch_attn_bwd_delta(const BwdParams& p, int dtype, int head_dim, hipStream_t stream);
 hipError_t launch_attn_bwd_dq(const BwdParams& p, int dtype, int head_dim, bool causal,

@@ -115,7 +115,7 @@ class DecodeStepArgs(ctypes.Structure):
 
 
 class Tuning(ctypes.Structure):
-    _fields_ = [("fwd_rows_per_wave", c_i32), ("decode_stages", c_i32), ("decode_waves", c_i32)]
+    _fields_ = [("tail_dynamic_pct", c_i32), ("decode_stages", c_i32), ("decode_waves", c_i32)]
 
 
 # (symbol, argtypes, restype) for every entry point the header declares.
@@ -216,7 +216,7 @@ def get_tuning() -> dict:
 @contextlib.contextmanager
 def tuning(**overrides) -> Iterator[dict]:
     """Run a block with some tuning fields replaced (pf_set_tuning), restoring
-    the previous values afterwards. Fields: fwd_rows_per_wave (32 | 64),
+    the previous values afterwards. Fields: tail_dynamic_pct (0..100),
     decode_stages (2..4), decode_waves (0 = one per resident slot, or the
     persistent decode grid size)."""
     old = get_tuning()
