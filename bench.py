@@ -29,16 +29,27 @@ over the timed launches, after at least as many untimed ones as --warmup):
                 np.random.default_rng(0), 16384-page pool, -1-padded table,
                 unreferenced pages and tails NaN; bytes = valid K/V + q + o +
                 used table entries + lens
-  hbm_read_ceiling_gbs  a plain streaming read of 2 GiB (the best of a few
-                launch shapes): what a read-only HBM stream reaches on this
-                device; *_frac_read_ceiling relate decode/paged to it
+  hbm_read_ceiling_gbs  a plain streaming read of 2 GiB (the best of three
+                load forms -- non-temporal and temporal register loads and
+                direct global->LDS loads -- over a few launch shapes; each form's best
+                in hbm_read_by_form_gbs): what a read-only HBM stream reaches on
+                this device; *_frac_read_ceiling relate decode/paged to it
+  mfma_stream_ceiling_tflops  back-to-back bf16 32x32x16 MFMAs on register
+                operands (no memory traffic), the best of a few launch shapes:
+                the matrix-core rate this box sustains under a pure MFMA load;
+                *_frac_mfma_ceiling relate the prefill kernels to it (beside
+                *_frac_mfma, against the 2.5 PFLOP/s specification), so a slow
+                box and a slow kernel can be told apart
+  dq_tflops, dkv_tflops  the config 3 dQ and dK/dV kernels at their credits
+                (dQ 1 matmul, dK/dV 4 of the 7 the step credits)
 
 Synthetic inputs: N(0,1) from torch's CUDA generator seeded 0 (config 5's
 lengths and page permutation from numpy's default_rng(0)), cast to bf16.
 
 CPU baselines (reported, not targets; the float32 numpy oracle, timed on this
 host's cores on a bounded sample of each workload): "cpu_baseline" for config
-3 forward+backward, and secondary.cpu_baselines for config 2 (fused RoPE),
+3 forward+backward (a quarter of the heads, median of three passes after a
+warm-up), and secondary.cpu_baselines for config 2 (fused RoPE),
 config 4 (decode, per sequence on the sliced prefix) and config 5 (paged,
 per sequence on the gathered pages). "cores" is the number of host cores
 this process may run on; "blas_threads" numpy's BLAS thread count.
@@ -478,41 +489,80 @@ def cpu_baseline_aux(a):
     return out
 
 
+def _probe_lib():
+    import ctypes
+    probe = ctypes.CDLL(os.path.join(PKG_DIR, "pallas_flash", "libpf_bench_probe.so"))
+    probe.pf_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p]
+    probe.pf_probe_read.restype = ctypes.c_int
+    probe.pf_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    probe.pf_probe_mfma.restype = ctypes.c_int
+    return probe
+
+
+READ_FORMS = {0: "16-byte non-temporal register loads", 1: "16-byte temporal register loads",
+              2: "direct global->LDS loads (buffer_load_dwordx4 ... lds)",
+              3: "non-temporal direct global->LDS loads (the streaming decode's form)"}
+
+
+def _median_launch_ms(torch, call, iters, warm=3):
+    for _ in range(warm):
+        call()
+    ev = Events(2, iters)
+    for i in range(iters):
+        ev.mark(i, 0)
+        call()
+        ev.mark(i, 1)
+    torch.cuda.synchronize()
+    return ev.median_ms(0, 1)
+
+
 def bench_read_ceiling(torch, iters):
     """The practical HBM read ceiling: a plain streaming read of a 2 GiB
-    buffer (16-byte non-temporal loads, 4 or 8 in flight per thread,
-    grid-stride over 2048-16384 workgroups of 256 threads; the probe library
-    built beside the attention library). The best configuration's median
-    time. Returns (GB/s, description)."""
-    import ctypes
-    path = os.path.join(PKG_DIR, "pallas_flash", "libpf_bench_probe.so")
-    probe = ctypes.CDLL(path)
-    fn = probe.pf_probe_stream_read
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    fn.restype = ctypes.c_int
+    buffer (grid-stride over 2048-16384 workgroups of 256 threads, 4 or 8
+    loads in flight per thread or wave) in four load forms: non-temporal and
+    temporal 16-byte register loads and direct global->LDS loads. Returns
+    (best GB/s, its description, {form: best GB/s})."""
+    probe = _probe_lib()
     nbytes = 2 << 30
     buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     buf.fill_(1)
     sink = torch.zeros(16384, dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
-    best = None
-    for unroll in (4, 8):
-        for blocks in (2048, 4096, 8192, 16384):
-            call = lambda: ok(fn(buf.data_ptr(), nbytes, sink.data_ptr(), blocks, unroll, st), "probe read")
-            for _ in range(3):
-                call()
-            ev = Events(2, iters)
-            for i in range(iters):
-                ev.mark(i, 0)
-                call()
-                ev.mark(i, 1)
-            torch.cuda.synchronize()
-            ms = float(np.median([e[0].elapsed_time(e[1]) for e in ev.ev]))
-            gbs = nbytes / (ms * 1e-3) / 1e9
-            if best is None or gbs > best[0]:
-                best = (gbs, f"{blocks} workgroups x 256 threads, {unroll} 16-byte non-temporal loads in flight "
-                             f"per thread, 2 GiB buffer, median of {iters}")
+    best, per_form = None, {}
+    for form, what in READ_FORMS.items():
+        for unroll in (4, 8):
+            for blocks in (2048, 4096, 8192, 16384):
+                call = lambda: ok(probe.pf_probe_read(buf.data_ptr(), nbytes, sink.data_ptr(), blocks, unroll,
+                                                      form, st), "probe read")
+                gbs = nbytes / (_median_launch_ms(torch, call, iters) * 1e-3) / 1e9
+                per_form[form] = max(per_form.get(form, 0.0), gbs)
+                if best is None or gbs > best[0]:
+                    best = (gbs, f"{what}, {blocks} workgroups x 256 threads, {unroll} in flight, 2 GiB buffer, "
+                                 f"median of {iters}")
     del buf, sink
+    return best[0], best[1], {READ_FORMS[f].split(" (")[0]: round(g, 1) for f, g in per_form.items()}
+
+
+def bench_mfma_ceiling(torch, iters):
+    """The same-run matrix-core ceiling: back-to-back 32x32x16 bf16 MFMAs on
+    register operands (four independent accumulators per wave, no memory
+    traffic) over 256-2048 workgroups of 256 threads; the best launch shape's
+    median TFLOP/s. Reads a box's sustained MFMA rate (its clock under a full
+    MFMA load included), against which the prefill kernels' rates are also
+    stated."""
+    probe = _probe_lib()
+    it = 8192
+    best = None
+    for blocks in (256, 512, 1024, 2048):
+        out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+        st = torch.cuda.current_stream().cuda_stream
+        call = lambda: ok(probe.pf_probe_mfma(out.data_ptr(), blocks, it, st), "probe mfma")
+        ms = _median_launch_ms(torch, call, iters)
+        tflops = blocks * 4 * it * 8 * 32768 / (ms * 1e-3) / 1e12
+        if best is None or tflops > best[0]:
+            best = (tflops, f"{blocks} workgroups x 4 waves, {8 * it} MFMAs per wave, median of {iters}")
+        del out
     return best
 
 
@@ -543,33 +593,46 @@ def _host_cores():
     return cores, int(blas)
 
 
-def cpu_baseline(c3):
+def cpu_baseline(c3, n_kv=2, reps=3):
     """The float32 numpy restatement of the reference algorithm (oracle/),
-    forward + backward on a bounded sample of config 3: batch 0 (16 query
-    heads over 4 KV heads, half the batch), full S=8192 causal. Credited
-    FLOPs of the sample / wall time."""
+    forward + backward on a bounded sample of config 3: batch 0, KV heads
+    [0, n_kv) with their 4 query heads each (8 of 32 (b, h) heads), full
+    S=8192 causal. One untimed warm-up pass, then the median of `reps` timed
+    passes. Credited FLOPs of the sample (3.5 forwards, as on the GPU) / wall
+    time; the oracle's backward recomputes the attention to get P and the LSE,
+    so the CPU executes 9 S-sized matmuls per pass for the 7 credited."""
     import torch
     from oracle import attention_bwd_ref, attention_ref
     cores, blas = _host_cores()
     S, D = c3["S"], c3["D"]
     h = c3["host"]
+    g = c3["Hq"] // c3["Hkv"]
     f32 = lambda t: t.float().cpu().numpy()
-    q = f32(h["q"][0:1])
-    k = f32(h["k"][0:1])
-    v = f32(h["v"][0:1])
-    do = f32(h["do"][0:1])
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    attention_ref(q, k, v, causal=True, dtype=np.float32)
-    attention_bwd_ref(q, k, v, do, causal=True, dtype=np.float32)
-    dt = time.perf_counter() - t0
+    q = f32(h["q"][0:1, :n_kv * g])
+    k = f32(h["k"][0:1, :n_kv])
+    v = f32(h["v"][0:1, :n_kv])
+    do = f32(h["do"][0:1, :n_kv * g])
+    if torch.cuda.is_available():
+        torch.cuda.synchronize()
+
+    def one():
+        t0 = time.perf_counter()
+        o, _ = attention_ref(q, k, v, causal=True, dtype=np.float32)
+        attention_bwd_ref(q, k, v, do, causal=True, o=o, dtype=np.float32)
+        return time.perf_counter() - t0
+
+    one()  # warm-up: first-touch of the sample's buffers, BLAS thread start-up
+    times = [one() for _ in range(reps)]
+    dt = float(np.median(times))
     flops = 3.5 * fwd_flops(1, q.shape[1], D, causal_pairs(S))
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "blas_threads": blas,
             "kind": "port",
             "sample": f"numpy float32 restatement (oracle/attention.py) of reference.py + its "
-                      f"backward, fwd+bwd of config 3 batch 0 (16 of 32 (b, h) heads) at "
-                      f"S={S}, {dt:.1f} s wall; matmuls on {blas} BLAS threads, elementwise "
-                      f"ops on 1 thread, {cores} host cores available"}
+                      f"backward, fwd+bwd of config 3 batch 0, kv heads 0-{n_kv - 1} ({q.shape[1]} of 32 (b, h) "
+                      f"heads) at S={S}: median of {reps} passes after one warm-up "
+                      f"({', '.join(f'{t:.2f}' for t in times)} s); the oracle's backward recomputes "
+                      f"P and the LSE (9 S-sized matmuls per pass, 7 credited); matmuls on {blas} BLAS "
+                      f"threads, elementwise ops on 1 thread, {cores} host cores available"}
 
 
 def cpu_baseline_rope(r, n_kv=4):
@@ -674,7 +737,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "aux", "stream", "copy"],
+    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "aux", "stream", "mfma", "copy"],
                     default="all")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
@@ -754,9 +817,16 @@ def main():
 
     if args.only in ("all", "stream"):
         log("hbm read ceiling ...")
-        gbs, how = bench_read_ceiling(torch, iters)
+        gbs, how, forms = bench_read_ceiling(torch, iters)
         sec["hbm_read_ceiling_gbs"] = gbs
         sec["hbm_read_ceiling_config"] = how
+        sec["hbm_read_by_form_gbs"] = forms
+
+    if args.only in ("all", "mfma"):
+        log("mfma stream ceiling ...")
+        tf, how = bench_mfma_ceiling(torch, iters)
+        sec["mfma_stream_ceiling_tflops"] = tf
+        sec["mfma_stream_ceiling_config"] = how
 
     if args.only == "copy":
         log("copy calibration ...")
@@ -799,10 +869,23 @@ def main():
         for k in ("decode", "decode_step", "paged"):
             if f"{k}_gbs" in sec:
                 line["secondary"][f"{k}_frac_read_ceiling"] = round(sec[f"{k}_gbs"] / sec["hbm_read_ceiling_gbs"], 4)
+    ceil = sec.get("mfma_stream_ceiling_tflops")
+    rates = {}
     if "fwd_tflops" in sec:
-        line["secondary"]["fwd_frac_mfma"] = round(sec["fwd_tflops"] / PEAK_BF16_TFLOPS, 4)
+        rates["fwd"] = sec["fwd_tflops"]
     if "fwd_loop_tflops" in sec:
-        line["secondary"]["fwd_loop_frac_mfma"] = round(sec["fwd_loop_tflops"] / PEAK_BF16_TFLOPS, 4)
+        rates["fwd_loop"] = sec["fwd_loop_tflops"]
+    if c3 is not None:
+        for short, kern in (("dq", "pf_attn_bwd_dq_kernel"), ("dkv", "pf_attn_bwd_dkv_kernel")):
+            rates[short] = c3["credit"][kern] / (c3["kern_ms"][kern] * 1e-3) / 1e12
+        line["secondary"]["dq_tflops"] = round(rates["dq"], 3)
+        line["secondary"]["dkv_tflops"] = round(rates["dkv"], 3)
+    if "rope_tflops" in sec:
+        rates["rope"] = sec["rope_tflops"]
+    for k, r in rates.items():
+        line["secondary"][f"{k}_frac_mfma"] = round(r / PEAK_BF16_TFLOPS, 4)
+        if ceil:
+            line["secondary"][f"{k}_frac_mfma_ceiling"] = round(r / ceil, 4)
     if cpu_sec:
         line["secondary"]["cpu_baselines"] = cpu_sec
     print(json.dumps(line), flush=True)

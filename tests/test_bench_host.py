@@ -69,3 +69,16 @@ def test_aux_cpu_baselines_run_on_small_inputs():
     assert set(out) == {"kv_write", "paged_write", "rope_vjp"}
     for v in out.values():
         assert v["unit"] == "GB/s" and v["value"] > 0 and v["kind"] == "port" and v["cores"] >= 1
+
+
+def test_cfg3_cpu_baseline_runs_on_a_small_sample():
+    """The config 3 CPU leg (warm-up, then the median of the timed passes)
+    on a tiny stand-in for config 3's inputs."""
+    import torch
+    g = torch.Generator().manual_seed(0)
+    mk = lambda *s: torch.randn(s, generator=g).to(torch.bfloat16)
+    c3 = {"S": 64, "D": 32, "Hq": 8, "Hkv": 2,
+          "host": {"q": mk(2, 8, 64, 32), "k": mk(2, 2, 64, 32), "v": mk(2, 2, 64, 32), "do": mk(2, 8, 64, 32)}}
+    out = bench.cpu_baseline(c3, n_kv=2, reps=3)
+    assert out["unit"] == "TFLOP/s" and out["value"] > 0 and out["kind"] == "port"
+    assert "median of 3" in out["sample"] and "recomputes" in out["sample"]

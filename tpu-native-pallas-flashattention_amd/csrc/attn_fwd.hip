@@ -546,8 +546,8 @@ __global__ __launch_bounds__(256) void pf_rope_rotate_k_kernel(const T* __restri
   for (int j = 0; j < kHeadsPerThread; ++j) {
     if (j < nh) {
       const T* src = k + ((int64_t)(bh0 + j) * Sk + pos) * D + pc * EPC;
-      lo[j] = ldg16(src);
-      hi[j] = ldg16(src + D / 2);
+      lo[j] = ldg16_nt(src);  // each row is read once
+      hi[j] = ldg16_nt(src + D / 2);
     }
   }
 #pragma unroll

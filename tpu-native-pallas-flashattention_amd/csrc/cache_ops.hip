@@ -64,8 +64,8 @@ __global__ __launch_bounds__(256) void pf_kv_cache_write_kernel(KvWriteParams p,
   if (slot < 0) return;
   const T* src = static_cast<const T*>(which ? p.v : p.k) + (bh * p.L + i) * D + c * EPC;
   T* dst = static_cast<T*>(which ? p.v_cache : p.k_cache) + (bh * p.C + slot) * D + c * EPC;
-  stg16(dst, ldg16(src));
-  stg16(dst + D / 2, ldg16(src + D / 2));
+  stg16_nt(dst, ldg16_nt(src));
+  stg16_nt(dst + D / 2, ldg16_nt(src + D / 2));
 }
 
 // ---------------------------------------------------------------------------
@@ -94,8 +94,8 @@ __global__ __launch_bounds__(256) void pf_paged_cache_write_kernel(PagedWritePar
   const T* src = static_cast<const T*>(which ? p.v : p.k) + (bh * p.L + i) * D + c * EPC;
   T* dst = static_cast<T*>(which ? p.v_pages : p.k_pages) +
            (((int64_t)page * p.Hkv + kvh) * p.page_size + off) * D + c * EPC;
-  stg16(dst, ldg16(src));
-  stg16(dst + D / 2, ldg16(src + D / 2));
+  stg16_nt(dst, ldg16_nt(src));
+  stg16_nt(dst + D / 2, ldg16_nt(src + D / 2));
 }
 
 template <typename T, int D>

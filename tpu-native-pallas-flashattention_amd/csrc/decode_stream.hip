@@ -56,6 +56,10 @@ namespace {
 constexpr int kSK = 32;               // keys per stage
 constexpr int kRowB = 256;            // bytes per K/V row (128 16-bit elements)
 constexpr int kTileB = kSK * kRowB;   // 8 KB: one stage of K (or V)
+// K/V stages are loaded non-temporal: each cache or pool byte is read once
+// per call, and a read-once stream reaches a higher HBM rate that way
+// (bench.py's read-form probe).
+constexpr bool kKvNt = true;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
@@ -343,9 +347,9 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
       const i32x4 dv = make_desc(Vb + seq, (uint32_t)c.L * kRowB);
       const uint32_t rb = (uint32_t)kv0 * kRowB;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dma16(dk, rb + loff[i], ldk + 1024 * i);
+      for (int i = 0; i < 8; ++i) dma16<kKvNt>(dk, rb + loff[i], ldk + 1024 * i);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dma16(dv, rb + loff[i], ldv + 1024 * i);
+      for (int i = 0; i < 8; ++i) dma16<kKvNt>(dv, rb + loff[i], ldv + 1024 * i);
     } else {
       const int ps = p.page_size;
       const int64_t trow = (int64_t)c.b * p.pages_per_seq;
@@ -368,9 +372,9 @@ __global__ __launch_bounds__(64) void pf_decode_stream_kernel(DecodeParams p) {
         const i32x4 dv = make_desc(Vb + pbase, (uint32_t)(nvalid * kRowB));
         const uint32_t rb = (uint32_t)(kv0 - prow0) * kRowB;
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) dma16(dk, rb + loff[gi * kPer + j], ldk + 1024 * (gi * kPer + j));
+        for (int j = 0; j < kPer; ++j) dma16<kKvNt>(dk, rb + loff[gi * kPer + j], ldk + 1024 * (gi * kPer + j));
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) dma16(dv, rb + loff[gi * kPer + j], ldv + 1024 * (gi * kPer + j));
+        for (int j = 0; j < kPer; ++j) dma16<kKvNt>(dv, rb + loff[gi * kPer + j], ldv + 1024 * (gi * kPer + j));
       }
     }
   };

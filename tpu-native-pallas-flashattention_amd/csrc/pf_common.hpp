@@ -176,16 +176,26 @@ __device__ inline i32x4 make_desc(const void* base, uint32_t bytes) {
 // an SGPR read by a VMEM instruction needs 5 wait states) and the LDS address
 // travels in M0 (an SALU write of M0 read by an LDS DMA needs 1). s_nop 4
 // gives 5.
+// NT = true marks the load non-temporal (the nt cache-policy bit): for data
+// read once, such as a decode step's K/V stream, which should not displace
+// reused lines from the caches.
+template <bool NT = false>
 __device__ inline void dma16(const i32x4& desc, uint32_t voff, uint32_t lds_addr) {
   // readfirstlane pins the (uniform) descriptor to SGPRs at this point, where
   // register pressure could otherwise leave it in VGPRs.
   i32x4 sd;
 #pragma unroll
   for (int i = 0; i < 4; ++i) sd[i] = __builtin_amdgcn_readfirstlane(desc[i]);
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "{m0}"(lds_addr), "v"(voff), "s"(sd)
-               : "memory");
+  if constexpr (NT)
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "{m0}"(lds_addr), "v"(voff), "s"(sd)
+                 : "memory");
+  else
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "{m0}"(lds_addr), "v"(voff), "s"(sd)
+                 : "memory");
 }
 
 // Wait until at most N vector-memory loads of this wave are outstanding
@@ -202,6 +212,13 @@ __device__ inline uint32_t lds_u32(const void* p) {
 
 __device__ inline u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void stg16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+// Non-temporal forms, for streams touched once (copies into a cache or page
+// pool, a rotation pass): they reach a higher HBM rate than ordinary loads
+// and stores and leave the caches to data that is reused.
+__device__ inline u32x4 ldg16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ inline void stg16_nt(void* p, u32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p)); }
 __device__ inline u32x4 lds16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void sts16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
