@@ -143,6 +143,13 @@ static void test_decode() {
   a.cache_len = 65;
   EXPECT(pf_attn_decode(&a, NULL) == PF_ERR_INVALID, "decode cache_len");
   EXPECT(pf_attn_decode_workspace_size(&a) == 0, "decode ws of invalid args");
+  a = dec_ok();
+  a.head_dim = 96;
+  EXPECT(pf_attn_decode_workspace_size(&a) > 0, "decode head_dim 96 in place");
+  a.head_dim = 100;
+  EXPECT(pf_attn_decode(&a, NULL) == PF_ERR_UNSUPPORTED, "decode head_dim 100 (bf16)");
+  a.dtype = PF_DTYPE_F32;
+  EXPECT(pf_attn_decode_workspace_size(&a) > 0, "decode head_dim 100 (float32) in place");
 }
 
 static pf_paged_attn_args paged_ok() {

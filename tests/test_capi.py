@@ -165,7 +165,23 @@ def test_paged_workspace_and_rejections(L):
     assert L.pf_paged_attn(_paged(), None) == _lib.PF_ERR_WORKSPACE
     assert L.pf_paged_attn(_paged(num_heads=12), None) == _lib.PF_ERR_INVALID
     assert L.pf_paged_attn(_paged(context_lens=None, workspace=256, workspace_bytes=ws), None) == _lib.PF_ERR_INVALID
-    assert L.pf_paged_attn(_paged(head_dim=80), None) == _lib.PF_ERR_UNSUPPORTED
+    # any head_dim <= 128 whose rows are whole 16-byte chunks is read in place
+    assert L.pf_paged_attn_workspace_size(_paged(head_dim=80)) > 0
+    assert L.pf_paged_attn_workspace_size(_paged(head_dim=96, dtype=0)) > 0
+    for bad in (dict(head_dim=84), dict(head_dim=136), dict(head_dim=0), dict(head_dim=6, dtype=0)):
+        assert L.pf_paged_attn(_paged(**bad), None) == _lib.PF_ERR_UNSUPPORTED, bad
+        assert L.pf_paged_attn_workspace_size(_paged(**bad)) == 0, bad
+
+
+def test_decode_head_dims_read_in_place(L):
+    """pf_attn_decode takes head_dim 8..128 in steps of one 16-byte chunk
+    (8 elements for 16-bit dtypes, 4 for float32); the workspace holds the
+    partials at the compute width (64 or 128)."""
+    for d, dt in ((80, 1), (96, 2), (8, 1), (36, 0), (100, 0)):
+        ws = L.pf_attn_decode_workspace_size(_dec(head_dim=d, dtype=dt))
+        assert ws > 0 and ws % 256 == 0, (d, dt)
+    for d, dt in ((84, 1), (100, 1), (6, 0), (132, 0)):
+        assert L.pf_attn_decode(_dec(head_dim=d, dtype=dt), None) == _lib.PF_ERR_UNSUPPORTED, (d, dt)
 
 
 def test_status_mapping():

@@ -119,6 +119,93 @@ def test_paged_head_dim_32(dt):
     check_fwd(host(out), paged_ref(host(tq), host(tk), host(tv), table, lens), dt)
 
 
+def _peak_extra(fn):
+    """Run fn; return (its result, device bytes allocated at the peak beyond
+    what was allocated before the call)."""
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    out = fn()
+    torch.cuda.synchronize()
+    return out, torch.cuda.max_memory_allocated() - before
+
+
+@pytest.mark.parametrize("d,dt", [(96, "bf16"), (80, "bf16"), (80, "f16"), (96, "f32"), (36, "f32")])
+def test_decode_head_dim_read_in_place(d, dt):
+    """Decode at a head_dim the kernels read in place: checked against the
+    oracle, NaN past cache_len, and no cache-sized allocation in the call."""
+    note(f"shapes: decode in place head_dim={d} dt={dt}")
+    rng = np.random.default_rng(d)
+    B, Hq, Hkv, cap, L = 4, 16, 4, 2048, 1500
+    q = rng.standard_normal((B, Hq, 1, d))
+    kc = rng.standard_normal((B, Hkv, cap, d))
+    vc = rng.standard_normal((B, Hkv, cap, d))
+    kc[:, :, L:] = np.nan
+    vc[:, :, L:] = np.nan
+    tq, tk, tv = dev(q, dt), dev(kc, dt), dev(vc, dt)
+    out, extra = _peak_extra(lambda: flash_attention_decode(tq, tk, tv, L))
+    cache_bytes = tk.numel() * tk.element_size()
+    assert extra < cache_bytes // 4, f"call allocated {extra} bytes beside a {cache_bytes}-byte cache"
+    assert out.shape == (B, Hq, 1, d)
+    check_fwd(host(out), decode_ref(host(tq), host(tk)[:, :, :L], host(tv)[:, :, :L], L), dt)
+
+
+@pytest.mark.parametrize("d,dt", [(96, "bf16"), (80, "bf16"), (80, "f32")])
+def test_paged_head_dim_read_in_place(d, dt):
+    """Paged decode at a head_dim the kernels read in place over a scrambled,
+    -1-padded table with NaN in unreferenced pages: checked against the oracle
+    and no pool-sized allocation in the call."""
+    note(f"shapes: paged in place head_dim={d} dt={dt}")
+    rng = np.random.default_rng(d + 1)
+    num_pages, page, pps, B, Hq, Hkv = 512, 16, 40, 8, 16, 4
+    kp = rng.standard_normal((num_pages, Hkv, page, d))
+    vp = rng.standard_normal((num_pages, Hkv, page, d))
+    lens = rng.integers(1, pps * page + 1, size=B).astype(np.int32)
+    table = np.full((B, pps), -1, np.int32)
+    perm = rng.permutation(num_pages)
+    used = 0
+    for b in range(B):
+        n = -(-int(lens[b]) // page)
+        table[b, :n] = perm[used:used + n]
+        used += n
+    unused = perm[used:]
+    kp[unused] = np.nan
+    vp[unused] = np.nan
+    for b in range(B):  # rows past each sequence's length in its last page
+        n, r = -(-int(lens[b]) // page), int(lens[b]) % page
+        if r:
+            kp[table[b, n - 1], :, r:] = np.nan
+            vp[table[b, n - 1], :, r:] = np.nan
+    q = rng.standard_normal((B, Hq, 1, d))
+    tq, tk, tv = dev(q, dt), dev(kp, dt), dev(vp, dt)
+    tt, tl = torch.as_tensor(table).to(DEV), torch.as_tensor(lens).to(DEV)
+    out, extra = _peak_extra(lambda: paged_flash_attention(tq, tk, tv, tt, tl))
+    pool_bytes = tk.numel() * tk.element_size()
+    assert extra < pool_bytes // 4, f"call allocated {extra} bytes beside a {pool_bytes}-byte pool"
+    check_fwd(host(out), paged_ref(host(tq), np.nan_to_num(host(tk)), np.nan_to_num(host(tv)), table, lens), dt)
+
+
+def test_decode_head_dim_copy_path_warns():
+    """A head_dim the kernels cannot read in place (100 in bfloat16: rows of
+    200 bytes) still computes correctly through the padded copy, and says so
+    once."""
+    note("shapes: decode head_dim=100 bf16 copy path")
+    import warnings
+    from pallas_flash import _shape
+    _shape._warned.discard("flash_attention_decode")
+    rng = np.random.default_rng(100)
+    q = rng.standard_normal((2, 4, 1, 100))
+    kc = rng.standard_normal((2, 2, 64, 100))
+    vc = rng.standard_normal((2, 2, 64, 100))
+    tq, tk, tv = dev(q, "bf16"), dev(kc, "bf16"), dev(vc, "bf16")
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        out = flash_attention_decode(tq, tk, tv, 50)
+        flash_attention_decode(tq, tk, tv, 50)
+    assert sum("copied on every call" in str(x.message) for x in w) == 1
+    check_fwd(host(out), decode_ref(host(tq), host(tk)[:, :, :50], host(tv)[:, :, :50], 50), "bf16")
+
+
 def test_rope_head_dim_96_forward_backward():
     note("shapes: rope head_dim=96 f32 causal")
     rng = np.random.default_rng(96)

@@ -46,6 +46,16 @@ Tuning& tuning() {
 bool dtype_ok(int32_t d) { return d == PF_DTYPE_F32 || d == PF_DTYPE_BF16 || d == PF_DTYPE_F16; }
 bool head_dim_ok(int32_t d) { return d == 64 || d == 128; }
 
+// Decode and paged decode also read rows of any head_dim up to 128 that are
+// whole 16-byte chunks (a multiple of 8 elements for bf16/f16, 4 for float32)
+// in place: the generic kernel computes at 64 or 128 with the missing columns
+// as zeros. dtype must already be valid.
+bool decode_head_dim_ok(int32_t d, int32_t dtype) {
+  const int32_t es = dtype == PF_DTYPE_F32 ? 4 : 2;
+  return d >= 1 && d <= 128 && (d * es) % 16 == 0;
+}
+int32_t decode_compute_dim(int32_t d) { return d <= 64 ? 64 : 128; }
+
 constexpr int64_t kMaxGrid = 0x7fffffff;
 
 int check_attn_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, int32_t D,
@@ -345,7 +355,7 @@ static int fill_decode(const pf_attn_decode_args* a, pf::DecodeParams* p) {
   if (a->cache_len < 1 || a->cache_len > a->cache_size) return PF_ERR_INVALID;
   if (!isfinite(a->sm_scale)) return PF_ERR_INVALID;
   if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
-  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if (!decode_head_dim_ok(a->head_dim, a->dtype)) return PF_ERR_UNSUPPORTED;
   const int g = a->num_heads / a->num_kv_heads;
   const int64_t units = (int64_t)a->batch * a->num_kv_heads * ((g + 31) / 32);
   *p = pf::DecodeParams{};
@@ -356,7 +366,8 @@ static int fill_decode(const pf_attn_decode_args* a, pf::DecodeParams* p) {
   p->B = a->batch;
   p->Hq = a->num_heads;
   p->Hkv = a->num_kv_heads;
-  p->D = a->head_dim;
+  p->D = decode_compute_dim(a->head_dim);
+  p->dr = a->head_dim;
   p->cache_size = a->cache_size;
   p->cache_len = a->cache_len;
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
@@ -420,7 +431,7 @@ static int fill_paged(const pf_paged_attn_args* a, pf::DecodeParams* p) {
   if (a->num_heads % a->num_kv_heads != 0) return PF_ERR_INVALID;
   if (!isfinite(a->sm_scale)) return PF_ERR_INVALID;
   if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
-  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if (!decode_head_dim_ok(a->head_dim, a->dtype)) return PF_ERR_UNSUPPORTED;
   const int64_t max_len = (int64_t)a->pages_per_seq * a->page_size;
   if (max_len > 0x7fffffff) return PF_ERR_UNSUPPORTED;
   const int g = a->num_heads / a->num_kv_heads;
@@ -435,7 +446,8 @@ static int fill_paged(const pf_paged_attn_args* a, pf::DecodeParams* p) {
   p->B = a->batch;
   p->Hq = a->num_heads;
   p->Hkv = a->num_kv_heads;
-  p->D = a->head_dim;
+  p->D = decode_compute_dim(a->head_dim);
+  p->dr = a->head_dim;
   p->num_pages = a->num_pages;
   p->page_size = a->page_size;
   p->pages_per_seq = a->pages_per_seq;
@@ -599,7 +611,8 @@ static int fill_decode_step(const pf_attn_decode_step_args* a, pf::DecodeParams*
   p->B = a->batch;
   p->Hq = a->num_heads;
   p->Hkv = a->num_kv_heads;
-  p->D = a->head_dim;
+  p->D = decode_compute_dim(a->head_dim);
+  p->dr = a->head_dim;
   p->cache_size = a->cache_size;
   p->cache_len = a->cache_size;
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;

@@ -38,16 +38,17 @@ __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <typename T, int D, bool PAGED>
+// Row `key` of (b, kv head) in the cache or pool; rows are p.dr elements.
+template <typename T, bool PAGED>
 __device__ inline const T* key_row(const DecodeParams& p, const T* base, int b, int kvh, int key) {
   if constexpr (PAGED) {
     const int lp = key / p.page_size;
     int page = p.block_tables[(int64_t)b * p.pages_per_seq + lp];
     page = min(max(page, 0), p.num_pages - 1);
     const int off = key - lp * p.page_size;
-    return base + (((int64_t)page * p.Hkv + kvh) * p.page_size + off) * D;
+    return base + (((int64_t)page * p.Hkv + kvh) * p.page_size + off) * p.dr;
   } else {
-    return base + ((int64_t)(b * p.Hkv + kvh) * p.cache_size + key) * D;
+    return base + ((int64_t)(b * p.Hkv + kvh) * p.cache_size + key) * p.dr;
   }
 }
 
@@ -104,13 +105,17 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
   const T* Kbase = static_cast<const T*>(p.k);
   const T* Vbase = static_cast<const T*>(p.v);
 
+  // Stored head dim: columns [dr, D) are zeros (never read).
+  const int dr = p.dr;
+  auto col_ok = [&](int col) { return col < dr; };  // col: first column of a 16-byte chunk
+
   // Q fragment (B operand): lane holds Q[b, h, 0, hh*HALF .. +HALF)
   Frag qf[QF];
   {
-    const T* qr = static_cast<const T*>(p.q) + (int64_t)(b * p.Hq + h) * D + hh * HALF;
+    const T* qr = static_cast<const T*>(p.q) + (int64_t)(b * p.Hq + h) * dr + hh * HALF;
 #pragma unroll
     for (int c = 0; c < HALF / EPC; ++c) {
-      const u32x4 ch = qvalid ? ldg16(qr + c * EPC) : (u32x4){0u, 0u, 0u, 0u};
+      const u32x4 ch = (qvalid && col_ok(hh * HALF + c * EPC)) ? ldg16(qr + c * EPC) : (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
       for (int f = 0; f < FPC; ++f) qf[c * FPC + f] = chunk_frag<T>(ch, f);
     }
@@ -129,9 +134,10 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     for (int t = 0; t < 2; ++t) {
       const int key = kv0 + 32 * ((l32 >> 2) & 1) + 16 * t + 4 * (l32 >> 3) + (l32 & 3);
       if (key < k_end) {
-        const T* kr = key_row<T, D, PAGED>(p, Kbase, b, kvh, key) + hh * HALF;
+        const T* kr = key_row<T, PAGED>(p, Kbase, b, kvh, key) + hh * HALF;
 #pragma unroll
-        for (int c = 0; c < HALF / EPC; ++c) kc[t][c] = ldg16(kr + c * EPC);
+        for (int c = 0; c < HALF / EPC; ++c)
+          kc[t][c] = col_ok(hh * HALF + c * EPC) ? ldg16(kr + c * EPC) : (u32x4){0u, 0u, 0u, 0u};
       } else {
 #pragma unroll
         for (int c = 0; c < HALF / EPC; ++c) kc[t][c] = (u32x4){0u, 0u, 0u, 0u};
@@ -148,8 +154,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kv0 + 4 * kg + r;
-        if ((16 * NDC % 64 == 0 || c < 16 * NDC) && key < k_end)
-          vc[u][r] = ldg16(key_row<T, D, PAGED>(p, Vbase, b, kvh, key) + dc * EPC);
+        if ((16 * NDC % 64 == 0 || c < 16 * NDC) && key < k_end && col_ok(dc * EPC))
+          vc[u][r] = ldg16(key_row<T, PAGED>(p, Vbase, b, kvh, key) + dc * EPC);
         else
           vc[u][r] = (u32x4){0u, 0u, 0u, 0u};
       }
@@ -302,9 +308,12 @@ __global__ __launch_bounds__(256) void pf_decode_combine_kernel(DecodeParams p) 
     for (int e = 0; e < PER; ++e) o[e] += po[(int64_t)s * D + lane * PER + e] * w;
   }
   const float safe = (lsum == 0.f) ? 1.f : lsum;
-  T* out = static_cast<T*>(p.o) + (int64_t)bh * D + lane * PER;
+  T* out = static_cast<T*>(p.o) + (int64_t)bh * p.dr;
 #pragma unroll
-  for (int e = 0; e < PER; ++e) out[e] = Elem<T>::from_f32(o[e] / safe);
+  for (int e = 0; e < PER; ++e) {
+    const int col = lane * PER + e;
+    if (col < p.dr) out[col] = Elem<T>::from_f32(o[e] / safe);
+  }
 }
 
 template <typename T, int D, bool PAGED>
@@ -349,7 +358,8 @@ hipError_t launch_decode_combine(const DecodeParams& p, int dtype, bool paged, h
 }
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, bool paged, hipStream_t stream) {
-  if (decode_stream_supported(dtype, p.D, paged, p.page_size))
+  // the streaming kernel reads rows of exactly its compute width
+  if (p.dr == p.D && decode_stream_supported(dtype, p.dr, paged, p.page_size))
     return launch_decode_stream(p, dtype, paged, stream);
   hipError_t e = paged ? launch_dtype<true>(p, dtype, false, stream) : launch_dtype<false>(p, dtype, false, stream);
   if (e != hipSuccess) return e;

@@ -157,7 +157,12 @@ struct DecodeParams {
   const int32_t* context_lens;  // paged: [B] lengths; contiguous: null
   float* part_o;                // [B, Hq, n_split, D] partial (unnormalised) outputs
   float* part_ml;               // [B, Hq, n_split, 2] partial (max, sum)
-  int B, Hq, Hkv, D;
+  int B, Hq, Hkv, D;  // D: the compute head dim (64 or 128)
+  // Stored head dim: the row length of q, the cache or pool and o (the
+  // generic kernel reads rows of dr elements, dr <= D a multiple of one
+  // 16-byte chunk, and treats columns [dr, D) as zeros; the streaming
+  // kernel needs dr == D).
+  int dr;
   int cache_size;     // contiguous: slots per (b, kvh); paged: unused
   int cache_len;      // contiguous: valid slots
   int num_pages, page_size, pages_per_seq;  // paged only

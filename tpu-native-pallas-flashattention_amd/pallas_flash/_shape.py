@@ -17,12 +17,18 @@ operands. The API bridges the two on the device:
   combination (mixed dtypes, or float64) is computed in float32, as the
   reference computes, and the output is cast to q's dtype.
 
-Padding copies the padded operands (for decode and paged decode that is the
-whole cache or page pool, per call); callers on the fast path use head_dim 64
-or 128 and one dtype, where every step here is a no-op.
+Decode and paged decode read any head_dim up to 128 whose rows are whole
+16-byte chunks (a multiple of 8 for bfloat16/float16, of 4 for float32) in
+place (decode_head_dim): the generic decode kernel computes at 64 or 128 with
+the missing columns as zeros, so the cache or page pool is not copied. Other
+head dims there, and mixed dtypes, copy the padded or cast cache or pool per
+call, with a one-time warning (warn_copy). Prefill pads its operands, which
+are per-call inputs anyway.
 """
 
 from __future__ import annotations
+
+import warnings
 
 import torch
 import torch.nn.functional as F
@@ -40,6 +46,29 @@ def kernel_head_dim(head_dim: int) -> int:
         return 128
     raise NotImplementedError(
         f"head_dim {head_dim} is not supported (the kernels cover head_dim <= 128)")
+
+
+def decode_head_dim(head_dim: int, dtype: torch.dtype) -> int:
+    """The head_dim the decode / paged kernels are called with: the caller's
+    own when they read its rows in place (<= 128, rows of whole 16-byte
+    chunks), else the padded kernel size."""
+    es = torch.empty((), dtype=dtype).element_size()
+    if 0 < head_dim <= 128 and (head_dim * es) % 16 == 0:
+        return head_dim
+    return kernel_head_dim(head_dim)
+
+
+_warned = set()
+
+
+def warn_copy(what: str, reason: str) -> None:
+    """Warn (once per process and call site) that a call copies its cache or
+    pool because of its head_dim or dtypes."""
+    if what not in _warned:
+        _warned.add(what)
+        warnings.warn(f"{what}: {reason}; the cache/pool is copied on every call (use one dtype "
+                      f"and a head_dim <= 128 that is a multiple of 8 (16-bit) or 4 (float32) to avoid it)",
+                      RuntimeWarning, stacklevel=3)
 
 
 def compute_dtype(*tensors: torch.Tensor) -> torch.dtype:

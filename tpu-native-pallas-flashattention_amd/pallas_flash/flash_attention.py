@@ -32,7 +32,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._shape import adapt, compute_dtype, kernel_head_dim, restore
+from ._shape import adapt, compute_dtype, decode_head_dim, kernel_head_dim, restore, warn_copy
 
 
 def _validate(q, k, v, kv_len):
@@ -220,7 +220,11 @@ def flash_attention_decode(
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
     _lib.require_device(q, k_cache, v_cache)
-    cdt, dp = compute_dtype(q, k_cache, v_cache), kernel_head_dim(head_dim)
+    cdt = compute_dtype(q, k_cache, v_cache)
+    dp = decode_head_dim(head_dim, cdt)
+    if dp != head_dim or k_cache.dtype != cdt or v_cache.dtype != cdt:
+        warn_copy("flash_attention_decode", f"head_dim {head_dim} / dtypes {q.dtype}, {k_cache.dtype}, "
+                  f"{v_cache.dtype} are not read in place")
     q2, k2, v2 = (adapt(x, cdt, dp).contiguous() for x in (q, k_cache, v_cache))
     return restore(_decode(q2, k2, v2, cache_len, float(sm_scale)), head_dim, q.dtype)
 

@@ -23,7 +23,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._shape import adapt, compute_dtype, kernel_head_dim, restore
+from ._shape import adapt, compute_dtype, decode_head_dim, restore, warn_copy
 
 
 def paged_flash_attention(
@@ -49,8 +49,10 @@ def paged_flash_attention(
         interpret: accepted for compatibility; ignored.
 
     Returns:
-        ``[batch, num_heads, 1, head_dim]`` in q's dtype. head_dim other than
-        64/128 or mixed dtypes copy the pool padded/cast per call (``_shape``).
+        ``[batch, num_heads, 1, head_dim]`` in q's dtype. Any head_dim up to
+        128 that is a multiple of 8 (bfloat16/float16) or 4 (float32) is read
+        in place; other head dims and mixed dtypes copy the pool padded/cast
+        per call, with a one-time warning (``_shape``).
     """
     # paged.py:129-149
     if q.dim() != 4 or q.shape[2] != 1:
@@ -81,7 +83,11 @@ def paged_flash_attention(
     tables = block_tables.to(device=dev, dtype=torch.int32).contiguous()
     lens = context_lens.to(device=dev, dtype=torch.int32).contiguous()
     out_dtype = q.dtype
-    cdt, dp = compute_dtype(q, k_pages, v_pages), kernel_head_dim(head_dim)
+    cdt = compute_dtype(q, k_pages, v_pages)
+    dp = decode_head_dim(head_dim, cdt)
+    if dp != head_dim or k_pages.dtype != cdt or v_pages.dtype != cdt:
+        warn_copy("paged_flash_attention", f"head_dim {head_dim} / dtypes {q.dtype}, {k_pages.dtype}, "
+                  f"{v_pages.dtype} are not read in place")
     q, k_pages, v_pages = (adapt(x, cdt, dp).contiguous() for x in (q, k_pages, v_pages))
     o = torch.empty_like(q)
     if batch == 0:
