@@ -257,12 +257,15 @@ int pf_paged_attn(const pf_paged_attn_args* args, void* stream);
  *    streaming kernel) needs at most about 16.3 MiB at the default tuning on
  *    a 256-CU device, whatever the batch; the generic kernel needs about
  *    batch * num_heads * splits * 520 bytes.
+ *  - A call uses the array of the device `stream` belongs to (the null
+ *    stream's: the current device).
  *  - Every call on one GPU shares that GPU's array: calls that overlap on
  *    one GPU (different streams, or other host threads) race on it and must
  *    be serialised by the caller. Nothing carries over between calls.
  *  - The array's device address is resolved once per device
- *    (hipGetSymbolAddress) at the first call on it; no call allocates or
- *    frees.
+ *    (hipGetSymbolAddress, with that device current) at the first call on it,
+ *    also when that call is being recorded into a graph (the lookup runs
+ *    with the thread's capture mode relaxed); no call allocates or frees.
  * ------------------------------------------------------------------------- */
 #define PF_NOALLOC_SCRATCH_BYTES (32u << 20)
 int pf_paged_attn_noalloc(const pf_paged_attn_args* args, void* stream);

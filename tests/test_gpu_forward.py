@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import check_fwd, dev, host, max_abs, note, qkv, rel_err
+from gpu_util import DEV, check_fwd, dev, host, max_abs, note, qkv, rel_err
 from oracle import attention_ref
 from pallas_flash import flash_attention, flash_attention_with_lse
 
@@ -188,3 +188,32 @@ def test_pair_grouped_work_order(B, Hq, Hkv, S, causal):
     ref, ref_lse = attention_ref(host(tq), host(tk), host(tv), causal=causal)
     check_fwd(host(out), ref, "bf16")
     assert max_abs(host(lse), ref_lse) <= 1e-3
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(4, 16, 8, 4096), (2, 16, 8, 8192)])
+@pytest.mark.parametrize("pct", [0, 30])
+def test_pair_grouped_multi_group_order(B, Hq, Hkv, S, pct):
+    """Pairs whose K/V do not all fit an XCD's L2 at once: B=4 Hkv=8 S=4096
+    (2 MiB per pair, two of an XCD's four pairs at a time) and B=2 Hkv=8
+    S=8192 (4 MiB, one of two at a time), so fwd_work_item's later pair
+    groups run; with the static order (tail_dynamic_pct 0) and with the
+    default dynamic tail. Causal bf16; o and LSE of 96 sampled rows per head
+    against the oracle, and no row left unwritten (outputs NaN-filled)."""
+    from pallas_flash import _lib
+    note(f"pair groups > 0: B={B} Hq={Hq} Hkv={Hkv} S={S} tail {pct}%")
+    g = torch.Generator(device=DEV).manual_seed(S + B)
+    tq, tk, tv = (torch.randn(s, generator=g, device=DEV).to(torch.bfloat16)
+                  for s in ((B, Hq, S, 128), (B, Hkv, S, 128), (B, Hkv, S, 128)))
+    o = torch.full_like(tq, float("nan"))
+    lse = torch.full((B, Hq, S), float("nan"), device=DEV)
+    a = _lib.FwdArgs(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                     B, Hq, Hkv, S, S, 128, S, 1, 128 ** -0.5, _lib.dtype_tag(tq))
+    with _lib.tuning(tail_dynamic_pct=pct):
+        assert _lib.lib().pf_attn_fwd(a, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    rows = np.unique(np.concatenate([np.arange(0, S, S // 64), [1, 31, 32, 63, S - 33, S - 1],
+                                     np.random.default_rng(S).integers(0, S, 26)]))
+    ref, ref_lse = attention_ref(host(tq), host(tk), host(tv), causal=True, q_rows=rows)
+    check_fwd(host(o)[:, :, rows], ref, "bf16")
+    assert max_abs(host(lse)[:, :, rows], ref_lse) <= 1e-3

@@ -7,11 +7,17 @@ with a caller workspace, on two calls in a row where the second is smaller
 (bf16, page 64 and page 16), on a small persistent grid that cuts sequences
 across waves (partials in the array), and on the generic kernel (float32,
 page size 5); sizes past the array are refused before any launch.
+A call recorded into a HIP graph replays correctly while its inputs change
+in place, also when it is the process's first call of the entry point (the
+array's address is then looked up during the recording).
 """
 
 from __future__ import annotations
 
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -106,3 +112,54 @@ def test_noalloc_refuses_partials_past_the_array():
     assert st == _lib.PF_ERR_WORKSPACE
     torch.cuda.synchronize()
     assert bool((o == 3.0).all())
+
+
+def _graph_check(capture_first: bool) -> None:
+    """Record pf_paged_attn_noalloc into a graph (torch.cuda.graph) and replay
+    it four times with q and the pools rewritten in place; every replay
+    equals pf_paged_attn on the same inputs, bit for bit."""
+    L = _lib.lib()
+    q, kp, vp, tt, tl = _problem(70, 12, 32, 8, 64, 24, 12 * 24, "bf16", 24 * 64)
+    got = torch.full_like(q, float("nan"))
+    want = torch.full_like(q, float("nan"))
+    args = _args(q, kp, vp, tt, tl, got)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    if not capture_first:
+        with torch.cuda.stream(s):
+            assert L.pf_paged_attn_noalloc(ctypes.byref(args), s.cuda_stream) == _lib.PF_OK
+        torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        st = L.pf_paged_attn_noalloc(ctypes.byref(args), torch.cuda.current_stream().cuda_stream)
+    assert st == _lib.PF_OK, st
+    g = torch.Generator(device="cuda").manual_seed(71)
+    for it in range(4):
+        with torch.no_grad():
+            for t in (q, kp, vp):
+                t.copy_(torch.randn(t.shape, generator=g, device="cuda").to(t.dtype))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _with_workspace(L, _args(q, kp, vp, tt, tl, want), q)
+        assert torch.isfinite(want.float()).all()
+        assert torch.equal(got, want), f"replay {it} differs from pf_paged_attn"
+
+
+def test_noalloc_graph_replay():
+    note("noalloc graph replay")
+    _graph_check(capture_first=False)
+
+
+def test_noalloc_first_call_under_capture():
+    """In a fresh process whose first pf_paged_attn_noalloc call is being
+    recorded into a graph."""
+    note("noalloc first call under capture (child process)")
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([here, root, os.path.join(root, "tpu-native-pallas-flashattention_amd"),
+                                         env.get("PYTHONPATH", "")])
+    code = "import test_zz_no_alloc as t; t._graph_check(capture_first=True); print('child ok', flush=True)"
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "child ok" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]

@@ -508,13 +508,16 @@ struct ScratchAddr {
 };
 ScratchAddr g_scratch[kMaxScratchDevices];
 
-// Device address of the current device's `scratch` (PF_OK), resolved on the
-// first call on each device.
-int scratch_address(void** out) {
+// Device address of `scratch` on the device that `stream` belongs to (the
+// null stream's: the current device), resolved on the first call on each
+// device (symbol_address, with that device current, also under graph
+// capture).
+int scratch_address(hipStream_t stream, void** out) {
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return PF_ERR_LAUNCH;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return PF_ERR_LAUNCH;
   ScratchAddr& s = g_scratch[dev];
-  std::call_once(s.once, [&s] { s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch)); });
+  std::call_once(s.once, [&s, dev] { s.err = pf::symbol_address(dev, HIP_SYMBOL(scratch), &s.ptr); });
   if (s.err != hipSuccess || s.ptr == nullptr) return PF_ERR_LAUNCH;
   *out = s.ptr;
   return PF_OK;
@@ -534,7 +537,7 @@ int pf_paged_attn_noalloc(const pf_paged_attn_args* a, void* stream) {
   const size_t need = decode_ws_bytes(p);
   if (need > (size_t)PF_NOALLOC_SCRATCH_BYTES) return PF_ERR_WORKSPACE;
   void* ws = nullptr;
-  st = scratch_address(&ws);
+  st = scratch_address((hipStream_t)stream, &ws);
   if (st != PF_OK) return st;
   st = bind_workspace(&p, ws, PF_NOALLOC_SCRATCH_BYTES);
   if (st != PF_OK) return st;

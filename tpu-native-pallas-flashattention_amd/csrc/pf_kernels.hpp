@@ -30,6 +30,31 @@ struct WorkTail {
 // launches; work_tickets.hip), or null: launch without a dynamic tail.
 unsigned int* work_tickets(hipStream_t stream);
 
+// The device address of a file-scope __device__ variable (HIP_SYMBOL(x)) on
+// device `dev`: looked up with that device current (each device holds its
+// own copy), with this thread's stream-capture mode relaxed for the lookup so
+// that a first call made while a stream is recorded into a graph works too;
+// the current device and capture mode are restored. Inline, so the lookup is
+// compiled into the source file that defines the variable.
+inline hipError_t symbol_address(int dev, const void* symbol, void** out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return e;
+  if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  e = hipThreadExchangeStreamCaptureMode(&mode);
+  if (e == hipSuccess) {
+    e = hipGetSymbolAddress(out, symbol);
+    const hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
+    if (e == hipSuccess) e = e2;
+  }
+  if (cur != dev) {
+    const hipError_t e3 = hipSetDevice(cur);
+    if (e == hipSuccess) e = e3;
+  }
+  return e;
+}
+
 __host__ __device__ inline int work_tail_grid(const WorkTail& t, int n_work) {
   return t.tickets ? t.n_static + t.n_tickets : n_work;
 }

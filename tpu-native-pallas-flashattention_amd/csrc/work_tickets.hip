@@ -8,7 +8,8 @@
 // keeps one counter for all its launches. A launch recorded into a graph may
 // later run beside anything else, so it gets a counter of its own for the life
 // of the process. The counters are a static per-device array (zero at module
-// load), each on its own 128-byte line; when they run out, or the stream's
+// load), each on its own 128-byte line, whose device address is looked up
+// once per device (symbol_address); when they run out, or the stream's
 // capture state or device cannot be read, the caller launches without a
 // dynamic tail (every work item placed statically), which computes the same
 // result.
@@ -47,23 +48,10 @@ unsigned int* work_tickets(hipStream_t stream) {
   if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return nullptr;
   TicketSlots& s = g_slots[dev];
   std::lock_guard<std::mutex> lock(s.mu);
-  // The array's address is resolved at the first launch on the device that is
-  // not being recorded into a graph (a recording stream may forbid the module
-  // query); launches recorded before that run without a dynamic tail.
-  if (!s.resolved && cs == hipStreamCaptureStatusNone) {
+  if (!s.resolved) {
     s.resolved = true;
-    int cur = -1;
-    hipError_t e = hipGetDevice(&cur);
-    // the array's address on device `dev` (each device holds its own copy)
-    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
-    if (e == hipSuccess) {
-      e = hipGetSymbolAddress((void**)&s.base, HIP_SYMBOL(ticket_words));
-      if (cur != dev) {
-        const hipError_t e2 = hipSetDevice(cur);
-        if (e == hipSuccess) e = e2;
-      }
-    }
-    if (e != hipSuccess) s.base = nullptr;
+    void* base = nullptr;
+    if (symbol_address(dev, HIP_SYMBOL(ticket_words), &base) == hipSuccess) s.base = static_cast<unsigned int*>(base);
   }
   if (s.base == nullptr) return nullptr;
   int slot = -1;
