@@ -341,8 +341,8 @@ __global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_
     char* const kdst = kbuf0 + P * G::BYTES;
     char* const vdst = vbuf0 + (1 - P) * G::BYTES;
     const bool k_next = j + 2 < nblk;
-    const i32x4 kd = TileDma<T, D>::at_row(krs, kv1 + BN);
-    const i32x4 vd = TileDma<T, D>::at_row(vrs, kv1);
+    const i32x4 kd = TileDma<T, D>::pinned_at_row(krs, kv1 + BN);
+    const i32x4 vd = TileDma<T, D>::pinned_at_row(vrs, kv1);
     auto dma_part = [&](int i) __attribute__((always_inline)) {
       constexpr int PT = TileDma<T, D>::PER_T;
       if (i < PT) {

@@ -198,6 +198,34 @@ __device__ inline void dma16(const i32x4& desc, uint32_t voff, uint32_t lds_addr
                  : "memory");
 }
 
+// A burst of LDS DMA loads from one descriptor: dma_pin moves the descriptor
+// into SGPRs once (readfirstlane) and pads the VALU-writes-SGPR hazard there,
+// once, in an asm statement that takes the four values as tied operands, so
+// every use comes after the pad; dma16_pinned then pads only the M0 write
+// (1 wait state) in front of each load. The prefill kernels issue several
+// loads per descriptor, each of which dma16 pads with 5 wait states.
+__device__ inline i32x4 dma_pin(const i32x4& desc) {
+  int a = __builtin_amdgcn_readfirstlane(desc[0]);
+  int b = __builtin_amdgcn_readfirstlane(desc[1]);
+  int c = __builtin_amdgcn_readfirstlane(desc[2]);
+  int d = __builtin_amdgcn_readfirstlane(desc[3]);
+  asm volatile("s_nop 4" : "+s"(a), "+s"(b), "+s"(c), "+s"(d));
+  return (i32x4){a, b, c, d};
+}
+template <bool NT = false>
+__device__ inline void dma16_pinned(const i32x4& sd, uint32_t voff, uint32_t lds_addr) {
+  if constexpr (NT)
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "{m0}"(lds_addr), "v"(voff), "s"(sd)
+                 : "memory");
+  else
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "{m0}"(lds_addr), "v"(voff), "s"(sd)
+                 : "memory");
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding
 // (loads complete in issue order).
 template <int N>

@@ -86,15 +86,17 @@ struct TileDma {
     d[2] = (uint32_t)desc[2] > off ? (int)((uint32_t)desc[2] - off) : 0;
     return d;
   }
-  // Part u (of PER_T) of a tile load from a descriptor made by at_row: callers
-  // that spread a tile's loads over a compute sequence issue the parts one
-  // at a time.
+  // The descriptor of rows [row0, ...) pinned for a burst of loads (dma_pin).
+  __device__ static inline i32x4 pinned_at_row(const i32x4& desc, int row0) { return dma_pin(at_row(desc, row0)); }
+  // Part u (of PER_T) of a tile load from a descriptor made by pinned_at_row:
+  // callers that spread a tile's loads over a compute sequence issue the
+  // parts one at a time.
   __device__ inline void load_part(const i32x4& d, int u, char* tile) const {
-    dma16(d, voff[u], __builtin_amdgcn_readfirstlane(lds_u32(tile) + slot[u]));
+    dma16_pinned(d, voff[u], __builtin_amdgcn_readfirstlane(lds_u32(tile) + slot[u]));
   }
   // Rows [row0, row0 + 64) of the buffer `desc` describes.
   __device__ inline void load(const i32x4& desc, int row0, char* tile) const {
-    const i32x4 d = at_row(desc, row0);
+    const i32x4 d = pinned_at_row(desc, row0);
 #pragma unroll
     for (int u = 0; u < PER_T; ++u) load_part(d, u, tile);
   }
@@ -183,7 +185,10 @@ struct TrAddr {
 // are full). Hazards the compiler cannot see inside the assembly, with the
 // wait states this compiler's own gfx950 hazard model inserts for the
 // builtins: a VALU write of an A/B operand needs 2 before the MFMA reads it
-// (the s_nop 1 below); back-to-back MFMAs accumulating into the same
+// -- the callers' operands are LDS reads and fragments packed several MFMA
+// slots earlier, and a scan of the gfx950 assembly (tests/test_mfma_hazards.py)
+// checks that no VALU write of an operand comes within 2 wait states, so no
+// padding is issued; back-to-back MFMAs accumulating into the same
 // registers need none; an LDS load of an operand is waited for by the
 // compiler (it sees the operand). A VALU/memory read of the result needs 12
 // after the last MFMA: agpr_fence() before the accumulator is read. The
@@ -194,13 +199,13 @@ struct MfmaAgpr;
 template <>
 struct MfmaAgpr<bf16_t> {
   __device__ static inline void run(f32x16& acc, bf16x8 a, bf16x8 b) {
-    asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
   }
 };
 template <>
 struct MfmaAgpr<f16_t> {
   __device__ static inline void run(f32x16& acc, f16x8 a, f16x8 b) {
-    asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
   }
 };
 // 16 wait states before the compiler may read an AGPR accumulator written by
