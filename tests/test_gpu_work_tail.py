@@ -58,13 +58,16 @@ class _Step:
         return (self.o, self.lse, self.delta, self.dq, self.dk, self.dv)
 
     def run(self, stream=None):
+        """NaN-fill the outputs and launch the three kernels, all on `stream`
+        (default: the current stream), so the fill is ordered before them."""
         L = _lib.lib()
-        st = (stream or torch.cuda.current_stream()).cuda_stream
-        for t in self.outputs():
-            t.fill_(float("nan"))
-        assert L.pf_attn_fwd(ctypes.byref(self.fa), st) == 0
-        assert L.pf_attn_bwd_dq(ctypes.byref(self.ba), st) == 0
-        assert L.pf_attn_bwd_dkv(ctypes.byref(self.ba), st) == 0
+        s = stream or torch.cuda.current_stream()
+        with torch.cuda.stream(s):
+            for t in self.outputs():
+                t.fill_(float("nan"))
+            assert L.pf_attn_fwd(ctypes.byref(self.fa), s.cuda_stream) == 0
+            assert L.pf_attn_bwd_dq(ctypes.byref(self.ba), s.cuda_stream) == 0
+            assert L.pf_attn_bwd_dkv(ctypes.byref(self.ba), s.cuda_stream) == 0
 
 
 def _same(a, b):
@@ -102,6 +105,7 @@ def test_tail_on_two_streams():
         ref_a = [t.clone() for t in a.outputs()]
         ref_b = [t.clone() for t in b.outputs()]
     sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()  # the inputs, written on the default stream, are ready
     with _lib.tuning(tail_dynamic_pct=30):
         for _ in range(4):
             a.run(sa)

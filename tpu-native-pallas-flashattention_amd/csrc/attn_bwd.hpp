@@ -433,10 +433,11 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
     const int q = min(qb0 + (tid & (BMQ - 1)), p.Sq - 1);
     if (wv_u < 2 * NSUB) lreg = (wv_u < NSUB ? p.lse : p.delta)[qoff + q];
   };
+  // LDS holds lse in log2 units and -delta (the dP chains start from it).
   auto store_step = [&](char* buf, int qb0) {
     if (tid < 2 * BMQ) {
       const bool valid = qb0 + (tid & (BMQ - 1)) < p.Sq;
-      reinterpret_cast<float*>(buf + 2 * NSUB * G::BYTES)[tid] = valid ? (tid < BMQ ? lreg * kLog2e : lreg) : 0.f;
+      reinterpret_cast<float*>(buf + 2 * NSUB * G::BYTES)[tid] = valid ? (tid < BMQ ? lreg * kLog2e : -lreg) : 0.f;
     }
   };
 
@@ -569,13 +570,14 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       // MFMA i of pass U uses ring slot (ROFF + i) % 3: the index runs on
       // across the passes of a step
       constexpr int NT = 4 * NP, ROFF = (U * NT) % (LEAD + 1);
-      // The dP chains start at -delta (per query = per register), so they end
-      // as dP - delta and dS = P (dP - delta) needs no subtraction.
+      // The dP chains start at -delta (per query = per register; staged
+      // negated), so they end as dP - delta and dS = P (dP - delta) needs no
+      // subtraction.
       sx[0] = sx[1] = (f32x16)(0.f);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dx[t][r] = -dl[t][r >> 2][r & 3];
+        for (int r = 0; r < 16; ++r) dx[t][r] = dl[t][r >> 2][r & 3];
       // operand of MFMA i (i >= NT: MFMA i - NT of the next pass)
       auto read = [&](int i) __attribute__((always_inline)) {
         const int slot = (ROFF + i) % (LEAD + 1);
@@ -673,7 +675,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
               const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
               pv = ok ? pv : 0.f;
             }
-            dx[t][r] = pv * (dx[t][r] - dl[e]);
+            dx[t][r] = pv * (dx[t][r] + dl[e]);  // dl = -delta
             sx[t][r] = pv;
           }
         }
