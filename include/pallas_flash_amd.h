@@ -65,7 +65,9 @@ typedef enum { PF_DTYPE_F32 = 0, PF_DTYPE_BF16 = 1, PF_DTYPE_F16 = 2 } pf_dtype;
  * share of the items (the lightest) is instead handed out at run time to
  * whichever XCD is free, through a per-stream counter in a static device
  * array (no allocation; a launch recorded into a graph gets its own counter).
- * Results are bit-identical either way. Also applies to pf_attn_fwd_rope.
+ * Results are bit-identical either way. Also applies to pf_attn_fwd_rope and
+ * to the dQ kernel of pf_attn_bwd_dq / pf_attn_bwd (the dK/dV kernel places
+ * every item statically).
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* q;
@@ -382,9 +384,10 @@ int pf_attn_decode_step(const pf_attn_decode_step_args* args, void* stream);
  * arguments of its pallas_calls (flash_attention.py:479-490), which this
  * build accepts and ignores. Initial values come from the environment, read
  * once per process at the first launch or tuning call:
- *   PF_TAIL_DYNAMIC_PCT    0 .. 100: percentage of the forward's work items
- *                         handed out at run time to whichever XCD is free
- *                         (0: every item placed statically)
+ *   PF_TAIL_DYNAMIC_PCT   0 .. 100 (default 30): percentage of the forward's
+ *                         and dQ's work items (the lightest) handed out at run
+ *                         time to whichever XCD is free (0: every item placed
+ *                         statically; see pf_attn_fwd)
  *   PF_DECODE_STAGES      2 (default) .. 4: LDS ring depth of the streaming
  *                         decode / paged kernel
  *   PF_DECODE_WAVES       0 (default: one per resident slot, queried once per

@@ -332,8 +332,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hh = lane >> 5, l32 = lane & 31;
   // heavy first: for causal, early key blocks are attended by the most queries
-  const int w = work_tail_item(p.tail, n_kblk * p.B * p.Hkv, reinterpret_cast<int*>(smem));
-  if (w < 0) return;
+  const int w = blockIdx.x;
   const int kblk = w / (p.B * p.Hkv);
   const int bk = w % (p.B * p.Hkv);
   const int b = bk / p.Hkv, kvh = bk % p.Hkv;
@@ -758,7 +757,7 @@ hipError_t dq_typed(const BwdParams& p, bool causal, hipStream_t st) {
 template <typename T, int D>
 hipError_t dkv_typed(const BwdParams& p, bool causal, hipStream_t st) {
   const int n_kblk = (p.Sk + 127) / 128;
-  const dim3 grid(work_tail_grid(p.tail, bwd_dkv_items(p)));
+  const dim3 grid(bwd_dkv_items(p));
   if (causal)
     hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, true>), grid, dim3(256), 0, st, p, n_kblk);
   else

@@ -132,7 +132,10 @@ int fill_fwd(const pf_attn_fwd_args* a, pf::FwdParams* p) {
 // part is a multiple of the 8 XCDs so each gets the same number of its own
 // items. Launches of fewer than min_items items (two per resident workgroup
 // slot of the kernel) keep every item static, as do launches whose stream
-// gets no ticket counter.
+// gets no ticket counter. The dK/dV kernel, one workgroup per CU and two
+// items per CU, gains nothing from a tail (measured) and runs without one:
+// its items drawn by other XCDs only add HBM traffic (889 against 578 MB at
+// config 3).
 constexpr double kTailSlack = 2.0;
 
 pf::WorkTail plan_tail(int n_work, int min_items, hipStream_t stream) {
@@ -151,9 +154,8 @@ pf::WorkTail plan_tail(int n_work, int min_items, hipStream_t stream) {
 }
 
 // Minimum items for a dynamic tail: two per resident workgroup slot of a
-// 256-CU MI355X (the 16-bit forward and dQ run two workgroups per CU, dK/dV
-// one).
-constexpr int kTwoPerCu = 2 * 2 * 256, kOnePerCu = 2 * 256;
+// 256-CU MI355X (the 16-bit forward and dQ run two workgroups per CU).
+constexpr int kTwoPerCu = 2 * 2 * 256;
 
 }  // namespace
 
@@ -290,7 +292,6 @@ int pf_attn_bwd_dkv(const pf_attn_bwd_args* a, void* stream) {
   int st = fill_bwd(a, &p, true);
   if (st != PF_OK) return st;
   if ((int64_t)p.B * p.Hkv * p.Sk == 0) return PF_OK;
-  p.tail = plan_tail(pf::bwd_dkv_items(p), kOnePerCu, (hipStream_t)stream);
   return finish(pf::launch_attn_bwd_dkv(p, a->dtype, a->head_dim, a->causal != 0, (hipStream_t)stream));
 }
 
@@ -306,7 +307,7 @@ int pf_attn_bwd(const pf_attn_bwd_args* a, void* stream) {
     if (st != PF_OK) return st;
   }
   if ((int64_t)p.B * p.Hkv * p.Sk > 0) {
-    p.tail = plan_tail(pf::bwd_dkv_items(p), kOnePerCu, s);
+    p.tail = pf::WorkTail{nullptr, 0, 0};  // dK/dV runs without a tail (plan_tail)
     st = finish(pf::launch_attn_bwd_dkv(p, a->dtype, a->head_dim, a->causal != 0, s));
   }
   return st;

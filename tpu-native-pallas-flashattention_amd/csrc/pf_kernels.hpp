@@ -10,7 +10,7 @@
 
 namespace pf {
 
-// Dynamic tail of a prefill launch (forward, dQ, dK/dV). Workgroups are
+// Dynamic tail of a prefill launch (forward, dQ). Workgroups are
 // dispatched round-robin over the 8 XCDs, and each XCD starts its workgroups
 // in blockIdx order as its CUs free up; XCDs run at somewhat different
 // speeds, so with a fixed item per workgroup they finish apart (up to 5-8%
@@ -158,7 +158,7 @@ struct BwdParams {
   int B, Hq, Hkv, Sq, Sk, kv_len, g;
   float sm_scale;
   float scale_log2;
-  WorkTail tail;  // of the kernel being launched (dQ or dK/dV)
+  WorkTail tail;  // of the dQ kernel (the dK/dV kernel runs without one)
 };
 
 // Work items of the dQ kernel (128 query rows of one head) and of the dK/dV
