@@ -25,7 +25,10 @@
  *  - Data types: dtype tags PF_DTYPE_F32 / PF_DTYPE_BF16 / PF_DTYPE_F16 name
  *    the storage type of q/k/v/o (and do/dq/dk/dv); all arithmetic is float32
  *    (MFMA with float32 accumulation). LSE / delta are always float32.
- *  - head_dim must be 64 or 128.
+ *  - head_dim: 64 or 128 for the prefill entry points; pf_attn_decode,
+ *    pf_paged_attn and pf_paged_attn_noalloc take any head_dim up to 128
+ *    whose rows are whole 16-byte chunks (a multiple of 8 for bf16/f16, of
+ *    4 for float32) and read the cache or pool rows in place.
  */
 #ifndef PALLAS_FLASH_AMD_H
 #define PALLAS_FLASH_AMD_H
@@ -190,6 +193,10 @@ int pf_attn_bwd(const pf_attn_bwd_args* args, void* stream);
  *   q [batch, num_heads, 1, head_dim]; o same shape
  *   k_cache, v_cache [batch, num_kv_heads, cache_size, head_dim]
  *   cache_len in (0, cache_size]; slots >= cache_len are never read.
+ *   head_dim <= 128, a multiple of 8 (bf16/f16) or 4 (float32): rows are
+ *   read in place; bf16/f16 with head_dim 128 run the streaming kernel, other
+ *   head dims and float32 the generic kernel (computing at 64 or 128 with
+ *   the missing columns as zeros), with the same results to rounding.
  * workspace: at least pf_attn_decode_workspace_size(args) bytes, 256-byte
  * aligned device memory (contents on entry do not matter).
  * ------------------------------------------------------------------------- */
@@ -220,10 +227,10 @@ int pf_attn_decode(const pf_attn_decode_args* args, void* stream);
  * non-positive length gives o = 0. Table entries at logical pages at or past
  * ceil(len / page_size) are never read (so -1 padding is legal); live entries
  * are clamped into [0, num_pages). Any page_size >= 1 is accepted (the
- * reference has no restriction). bf16/f16 with head_dim 128 and page_size a
- * multiple of 4 run the streaming kernel (each 4-row load stays inside one
- * page); other page sizes, dtypes and head dims run the generic split-KV
- * kernel, with the same results to rounding.
+ * reference has no restriction). head_dim as pf_attn_decode. bf16/f16 with
+ * head_dim 128 and page_size a multiple of 4 run the streaming kernel (each
+ * 4-row load stays inside one page); other page sizes, dtypes and head dims
+ * run the generic split-KV kernel, with the same results to rounding.
  * workspace: at least pf_paged_attn_workspace_size(args) bytes.
  * ------------------------------------------------------------------------- */
 typedef struct {
