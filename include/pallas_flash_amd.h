@@ -67,10 +67,11 @@ typedef enum { PF_DTYPE_F32 = 0, PF_DTYPE_BF16 = 1, PF_DTYPE_F16 = 2 } pf_dtype;
  * order; with pf_tuning.tail_dynamic_pct > 0 and at least 1024 items, that
  * share of the items (the lightest) is instead handed out at run time to
  * whichever XCD is free, through a per-stream counter in a static device
- * array (no allocation; a launch recorded into a graph gets its own counter).
- * Results are bit-identical either way. Also applies to pf_attn_fwd_rope and
- * to the dQ kernel of pf_attn_bwd_dq / pf_attn_bwd (the dK/dV kernel places
- * every item statically).
+ * array (no allocation; a launch recorded into a graph gets its own counter,
+ * so two replays of one graph must not run at the same time -- replays of a
+ * graph on one stream are ordered). Results are bit-identical either way.
+ * Also applies to pf_attn_fwd_rope and to the dQ kernel of pf_attn_bwd_dq /
+ * pf_attn_bwd (the dK/dV kernel places every item statically).
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* q;
