@@ -261,6 +261,70 @@ def bench_decode(L, _lib, torch, iters, warmup):
             {"q": q, "k": kc, "v": vc, "kv_len": kv_len})
 
 
+def bench_d256(L, _lib, torch, steps, warmup, iters):
+    """head_dim 256 (bf16): config 3's prefill shape (forward, dQ, dK/dV as
+    one training step; mean per-kernel times over `steps` steps) and config
+    4's decode shape (median over `iters` launches). Not a north-star
+    configuration: the reference's callers all use head_dim 128."""
+    B, Hq, Hkv, S, D = 2, 16, 4, 8192, 256
+    g = torch.Generator(device="cuda").manual_seed(3)
+    mk = lambda *shape: torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+    q, k, v, do = mk(B, Hq, S, D), mk(B, Hkv, S, D), mk(B, Hkv, S, D), mk(B, Hq, S, D)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device="cuda")
+    delta = torch.empty_like(lse)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    scale = 1.0 / D ** 0.5
+    fa = _lib.FwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                      B, Hq, Hkv, S, S, D, S, 1, scale, 1)
+    ba = _lib.BwdArgs(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                      lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                      B, Hq, Hkv, S, S, D, S, 1, scale, 1)
+    st = torch.cuda.current_stream().cuda_stream
+    calls = [lambda: ok(L.pf_attn_fwd(fa, st), "pf_attn_fwd"),
+             lambda: ok(L.pf_attn_bwd_dq(ba, st), "pf_attn_bwd_dq"),
+             lambda: ok(L.pf_attn_bwd_dkv(ba, st), "pf_attn_bwd_dkv")]
+    for _ in range(warmup):
+        for c in calls:
+            c()
+    ev = Events(4, steps)
+    for i in range(steps):
+        for j, c in enumerate(calls):
+            ev.mark(i, j)
+            c()
+        ev.mark(i, 3)
+    torch.cuda.synchronize()
+    assert torch.isfinite(dk.float()).all() and torch.isfinite(dq.float()).all(), "head_dim 256 gradients"
+    F = fwd_flops(B, Hq, D, causal_pairs(S))
+    prefill = {"fwd_ms": ev.mean_ms(0, 1), "dq_ms": ev.mean_ms(1, 2), "dkv_ms": ev.mean_ms(2, 3),
+               "step_ms": ev.mean_ms(0, 3), "F": F}
+    del q, k, v, do, o, lse, delta, dq, dk, dv
+    # decode: config 4's shape at head_dim 256 (generic split-KV kernel)
+    B, Hq, Hkv, cap, kv_len = 64, 32, 8, 8192, 6000
+    qd = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    kc = torch.empty((B, Hkv, cap, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    for t in (kc, vc):
+        t[:, :, :kv_len].copy_(torch.randn((B, Hkv, kv_len, D), generator=g, device="cuda"))
+        t[:, :, kv_len:].fill_(float("nan"))
+    od = torch.empty_like(qd)
+    args = _lib.DecodeArgs(qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), od.data_ptr(), B, Hq, Hkv, cap,
+                           D, kv_len, 1.0 / D ** 0.5, 1, None, 0)
+    ws = _decode_args_and_ws(L, _lib, torch, args, L.pf_attn_decode_workspace_size)
+    for _ in range(max(3, warmup)):
+        ok(L.pf_attn_decode(args, st), "pf_attn_decode")
+    dev_ = Events(2, iters)
+    for i in range(iters):
+        dev_.mark(i, 0)
+        ok(L.pf_attn_decode(args, st), "pf_attn_decode")
+        dev_.mark(i, 1)
+    torch.cuda.synchronize()
+    assert torch.isfinite(od.float()).all(), "head_dim 256 decode output"
+    nbytes = B * Hkv * kv_len * D * 2 * 2 + 2 * B * Hq * D * 2
+    del ws, kc, vc
+    return prefill, (dev_.median_ms(0, 1), nbytes)
+
+
 def cfg5_layout():
     """Config 5's sequences and pool: lengths U[512, 8192] and the page
     permutation from np.random.default_rng(0), pages dealt out in order, table
@@ -737,8 +801,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "aux", "stream", "mfma", "copy"],
-                    default="all")
+    ap.add_argument("--only", choices=["all", "cfg3", "rope", "decode", "paged", "aux", "stream", "mfma", "copy",
+                                       "d256"], default="all")
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -814,6 +878,16 @@ def main():
             log("cpu baselines aux ...")
             cpu_sec.update(cpu_baseline_aux(ain))
         del ain
+
+    if args.only in ("all", "d256"):
+        log("head_dim 256 prefill and decode ...")
+        pre, (ms, nb) = bench_d256(L, _lib, torch, args.steps, args.warmup, iters)
+        sec["d256_kernel_ms"] = {k: round(pre[k], 4) for k in ("fwd_ms", "dq_ms", "dkv_ms")}
+        sec["d256_fwd_tflops"] = pre["F"] / (pre["fwd_ms"] * 1e-3) / 1e12
+        sec["d256_step_tflops"] = 3.5 * pre["F"] / (pre["step_ms"] * 1e-3) / 1e12
+        sec["d256_decode_gbs"] = nb / (ms * 1e-3) / 1e9
+        sec["d256_config"] = ("bf16 head_dim 256: prefill at config 3's shape (B=2 Hq=16 Hkv=4 S=8192 causal), "
+                              "decode at config 4's (B=64 Hq=32 Hkv=8 cache 8192, kv_len 6000)")
 
     if args.only in ("all", "stream"):
         log("hbm read ceiling ...")

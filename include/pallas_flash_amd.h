@@ -25,10 +25,13 @@
  *  - Data types: dtype tags PF_DTYPE_F32 / PF_DTYPE_BF16 / PF_DTYPE_F16 name
  *    the storage type of q/k/v/o (and do/dq/dk/dv); all arithmetic is float32
  *    (MFMA with float32 accumulation). LSE / delta are always float32.
- *  - head_dim: 64 or 128 for the prefill entry points; pf_attn_decode,
- *    pf_paged_attn and pf_paged_attn_noalloc take any head_dim up to 128
- *    whose rows are whole 16-byte chunks (a multiple of 8 for bf16/f16, of
- *    4 for float32) and read the cache or pool rows in place.
+ *  - head_dim: 64, 128, or (bf16/f16) 256 for the prefill and RoPE entry
+ *    points (a float32 tile of 256 columns would not fit the LDS double
+ *    buffers); pf_attn_decode, pf_paged_attn, pf_paged_attn_noalloc and the
+ *    cache writes take any head_dim up to 256 (bf16/f16) or 128 (float32)
+ *    whose rows are whole 16-byte chunks (a multiple of 8 for bf16/f16, of 4
+ *    for float32) and read or write the cache or pool rows in place. The
+ *    reference bounds no head_dim; other values return PF_ERR_UNSUPPORTED.
  */
 #ifndef PALLAS_FLASH_AMD_H
 #define PALLAS_FLASH_AMD_H
@@ -194,10 +197,11 @@ int pf_attn_bwd(const pf_attn_bwd_args* args, void* stream);
  *   q [batch, num_heads, 1, head_dim]; o same shape
  *   k_cache, v_cache [batch, num_kv_heads, cache_size, head_dim]
  *   cache_len in (0, cache_size]; slots >= cache_len are never read.
- *   head_dim <= 128, a multiple of 8 (bf16/f16) or 4 (float32): rows are
- *   read in place; bf16/f16 with head_dim 128 run the streaming kernel, other
- *   head dims and float32 the generic kernel (computing at 64 or 128 with
- *   the missing columns as zeros), with the same results to rounding.
+ *   head_dim <= 256 (bf16/f16) or 128 (float32), a multiple of 8 (bf16/f16)
+ *   or 4 (float32): rows are read in place; bf16/f16 with head_dim 128 run
+ *   the streaming kernel, other head dims and float32 the generic kernel
+ *   (computing at 64, 128 or 256 with the missing columns as zeros), with
+ *   the same results to rounding.
  * workspace: at least pf_attn_decode_workspace_size(args) bytes, 256-byte
  * aligned device memory (contents on entry do not matter).
  * ------------------------------------------------------------------------- */
@@ -294,7 +298,7 @@ int pf_paged_attn_noalloc(const pf_paged_attn_args* args, void* stream);
  *                   b * positions_stride (stride 0: one position for all).
  * A row whose slot is out of range (linear: pos + i outside [0, cache_size);
  * ring: pos + i < 0) is not written (the reference's dynamic_update_slice
- * would clamp it onto a valid slot instead).
+ * would clamp it onto a valid slot instead). head_dim as pf_attn_decode.
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* k;
@@ -322,6 +326,7 @@ int pf_kv_cache_write(const pf_kv_cache_write_args* args, void* stream);
  * its table entry lies outside [0, num_pages) (e.g. -1 padding). Rows of
  * different sequences that map to one (page, offset) race; the caller keeps
  * them distinct (pages shared between sequences are for read-only prefixes).
+ * head_dim as pf_attn_decode.
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* k;

@@ -193,8 +193,10 @@ static void test_cache_writes() {
   w.positions_stride = -1;
   EXPECT(pf_kv_cache_write(&w, NULL) == PF_ERR_INVALID, "kv write negative stride");
   w.positions_stride = 0;
-  w.head_dim = 48;
+  w.head_dim = 44;  // rows of whole 16-byte chunks only
   EXPECT(pf_kv_cache_write(&w, NULL) == PF_ERR_UNSUPPORTED, "kv write head_dim");
+  w.head_dim = 264;
+  EXPECT(pf_kv_cache_write(&w, NULL) == PF_ERR_UNSUPPORTED, "kv write head_dim above 256");
 
   EXPECT(pf_paged_cache_write(NULL, NULL) == PF_ERR_INVALID, "paged write NULL args");
   pf_paged_cache_write_args p;

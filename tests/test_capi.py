@@ -80,7 +80,10 @@ def _fwd(**over):
     (dict(num_kv_heads=0), _lib.PF_ERR_INVALID),
     (dict(q=None), _lib.PF_ERR_INVALID),
     (dict(sm_scale=float("nan")), _lib.PF_ERR_INVALID),
-    (dict(head_dim=96), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=96), _lib.PF_ERR_UNSUPPORTED),                  # kernels: 64, 128, 256 (16-bit)
+    (dict(head_dim=192), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=512), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=256, dtype=0), _lib.PF_ERR_UNSUPPORTED),        # float32 stops at 128
     (dict(dtype=7), _lib.PF_ERR_UNSUPPORTED),
 ])
 def test_fwd_rejects_on_host(L, over, status):
@@ -165,22 +168,30 @@ def test_paged_workspace_and_rejections(L):
     assert L.pf_paged_attn(_paged(), None) == _lib.PF_ERR_WORKSPACE
     assert L.pf_paged_attn(_paged(num_heads=12), None) == _lib.PF_ERR_INVALID
     assert L.pf_paged_attn(_paged(context_lens=None, workspace=256, workspace_bytes=ws), None) == _lib.PF_ERR_INVALID
-    # any head_dim <= 128 whose rows are whole 16-byte chunks is read in place
+    # any head_dim up to 256 (16-bit) or 128 (float32) whose rows are whole
+    # 16-byte chunks is read in place
     assert L.pf_paged_attn_workspace_size(_paged(head_dim=80)) > 0
     assert L.pf_paged_attn_workspace_size(_paged(head_dim=96, dtype=0)) > 0
-    for bad in (dict(head_dim=84), dict(head_dim=136), dict(head_dim=0), dict(head_dim=6, dtype=0)):
+    assert L.pf_paged_attn_workspace_size(_paged(head_dim=136)) > 0
+    assert L.pf_paged_attn_workspace_size(_paged(head_dim=256, dtype=2)) > 0
+    for bad in (dict(head_dim=84), dict(head_dim=264), dict(head_dim=0), dict(head_dim=6, dtype=0),
+                dict(head_dim=136, dtype=0)):
         assert L.pf_paged_attn(_paged(**bad), None) == _lib.PF_ERR_UNSUPPORTED, bad
         assert L.pf_paged_attn_workspace_size(_paged(**bad)) == 0, bad
 
 
 def test_decode_head_dims_read_in_place(L):
-    """pf_attn_decode takes head_dim 8..128 in steps of one 16-byte chunk
-    (8 elements for 16-bit dtypes, 4 for float32); the workspace holds the
-    partials at the compute width (64 or 128)."""
-    for d, dt in ((80, 1), (96, 2), (8, 1), (36, 0), (100, 0)):
+    """pf_attn_decode takes head_dim 8..256 (16-bit) or 4..128 (float32) in
+    steps of one 16-byte chunk (8 elements for 16-bit dtypes, 4 for
+    float32); the workspace holds the partials at the compute width (64,
+    128 or 256)."""
+    for d, dt in ((80, 1), (96, 2), (8, 1), (36, 0), (100, 0), (136, 1), (200, 2), (256, 1)):
         ws = L.pf_attn_decode_workspace_size(_dec(head_dim=d, dtype=dt))
         assert ws > 0 and ws % 256 == 0, (d, dt)
-    for d, dt in ((84, 1), (100, 1), (6, 0), (132, 0)):
+    # the generic kernel's partials are the compute width wide: 256 above 128
+    assert (L.pf_attn_decode_workspace_size(_dec(head_dim=136, dtype=1))
+            > L.pf_attn_decode_workspace_size(_dec(head_dim=96, dtype=1)))
+    for d, dt in ((84, 1), (100, 1), (6, 0), (132, 0), (264, 1), (256, 0)):
         assert L.pf_attn_decode(_dec(head_dim=d, dtype=dt), None) == _lib.PF_ERR_UNSUPPORTED, (d, dt)
 
 
@@ -208,7 +219,9 @@ def _kvw(**over):
     (dict(cache_size=0), _lib.PF_ERR_INVALID),
     (dict(positions=None), _lib.PF_ERR_INVALID),
     (dict(dtype=9), _lib.PF_ERR_UNSUPPORTED),
-    (dict(head_dim=96), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=84), _lib.PF_ERR_UNSUPPORTED),                   # rows of whole 16-byte chunks only
+    (dict(head_dim=264), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=132, dtype=0), _lib.PF_ERR_UNSUPPORTED),          # float32 stops at 128
     (dict(seq_len=0, k=None, v=None, positions=None), _lib.PF_OK),  # nothing to write
 ])
 def test_kv_cache_write_rejects_on_host(L, over, status):
@@ -230,6 +243,8 @@ def _pw(**over):
     (dict(block_tables=None), _lib.PF_ERR_INVALID),
     (dict(positions_stride=5), _lib.PF_ERR_INVALID),
     (dict(dtype=4), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=100), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=256, dtype=0), _lib.PF_ERR_UNSUPPORTED),
     (dict(pages_per_seq=0, block_tables=None), _lib.PF_OK),  # no page to write into
 ])
 def test_paged_cache_write_rejects_on_host(L, over, status):
@@ -281,6 +296,7 @@ def _rope_args(**over):
     (dict(inverse=2), _lib.PF_ERR_INVALID),
     (dict(sin=None), _lib.PF_ERR_INVALID),
     (dict(head_dim=96), _lib.PF_ERR_UNSUPPORTED),
+    (dict(head_dim=256, dtype=0), _lib.PF_ERR_UNSUPPORTED),
     (dict(seq_len=0, x=None, out=None), _lib.PF_OK),
 ])
 def test_rope_rejects_on_host(L, over, status):

@@ -42,6 +42,7 @@ SOURCES = {
     "attn_fwd.hip": [],
     "attn_bwd.hip": [],
     "attn_bwd_f32.hip": [],
+    "attn_bwd_d256.hip": [],
     "decode_stream.hip": [],
 }
 

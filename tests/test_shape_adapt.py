@@ -14,20 +14,49 @@ import pytest
 import torch
 
 from oracle import apply_rope_ref, attention_ref, precompute_rope_ref
-from pallas_flash._shape import (compute_dtype, kernel_head_dim, pad_head_dim, pad_rope_halves,
-                                 unpad_rope_halves)
+from pallas_flash._shape import (compute_dtype, decode_head_dim, kernel_head_dim, max_head_dim, pad_head_dim,
+                                 pad_rope_halves, unpad_rope_halves)
+
+BF, F16, F32 = torch.bfloat16, torch.float16, torch.float32
 
 
 @pytest.mark.parametrize("d,want", [(1, 64), (32, 64), (64, 64), (65, 128), (80, 128), (128, 128)])
-def test_kernel_head_dim(d, want):
-    assert kernel_head_dim(d) == want
+@pytest.mark.parametrize("dt", [BF, F16, F32])
+def test_kernel_head_dim(d, want, dt):
+    assert kernel_head_dim(d, dt) == want
 
 
-def test_head_dim_above_128_is_not_implemented():
-    with pytest.raises(NotImplementedError):
-        kernel_head_dim(256)
+@pytest.mark.parametrize("d,want", [(129, 256), (160, 256), (192, 256), (256, 256)])
+@pytest.mark.parametrize("dt", [BF, F16])
+def test_kernel_head_dim_above_128_16bit(d, want, dt):
+    assert kernel_head_dim(d, dt) == want
+
+
+def test_head_dim_limits():
+    """256 columns for the 16-bit kernels, 128 for float32 (the compute dtype
+    of float32 and mixed inputs); above that NotImplementedError."""
+    assert (max_head_dim(BF), max_head_dim(F16), max_head_dim(F32)) == (256, 256, 128)
+    for dt in (BF, F16):
+        with pytest.raises(NotImplementedError):
+            kernel_head_dim(257, dt)
+    for d in (129, 256):
+        with pytest.raises(NotImplementedError):
+            kernel_head_dim(d, F32)
     with pytest.raises(ValueError):
-        kernel_head_dim(0)
+        kernel_head_dim(0, BF)
+
+
+@pytest.mark.parametrize("d,dt,want", [
+    (96, BF, 96), (200, BF, 200), (256, F16, 256), (136, BF, 136),   # whole 16-byte chunks: in place
+    (100, BF, 128), (250, BF, 256), (33, BF, 64),                   # ragged chunks: padded
+    (132, F32, None),                                               # float32 above 128: unsupported
+    (124, F32, 124), (126, F32, 128)])
+def test_decode_head_dim(d, dt, want):
+    if want is None:
+        with pytest.raises(NotImplementedError):
+            decode_head_dim(d, dt)
+    else:
+        assert decode_head_dim(d, dt) == want
 
 
 def test_compute_dtype():
@@ -41,11 +70,11 @@ def test_compute_dtype():
     assert compute_dtype(f64, f64, f64) == torch.float32      # no float64 kernel
 
 
-@pytest.mark.parametrize("d", [32, 80, 96])
+@pytest.mark.parametrize("d", [32, 80, 96, 160])
 def test_zero_padding_keeps_attention(d):
     rng = np.random.default_rng(d)
     q, k, v = (rng.standard_normal((1, 2, 9, d)) for _ in range(3))
-    dp = kernel_head_dim(d)
+    dp = kernel_head_dim(d, BF)
     pad = lambda x: pad_head_dim(torch.from_numpy(x), dp).numpy()
     scale = 1.0 / d ** 0.5                          # the caller's head_dim sets the default scale
     o, lse = attention_ref(q, k, v, causal=True)
@@ -54,12 +83,12 @@ def test_zero_padding_keeps_attention(d):
     assert np.allclose(lsep, lse, atol=1e-12)
 
 
-@pytest.mark.parametrize("d", [32, 80, 96])
+@pytest.mark.parametrize("d", [32, 80, 96, 200])
 def test_rope_half_padding_commutes_with_rotation(d):
     rng = np.random.default_rng(d + 1)
     x = rng.standard_normal((1, 2, 7, d))
     cos, sin = precompute_rope_ref(7, d)
-    dp = kernel_head_dim(d)
+    dp = kernel_head_dim(d, BF)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
     xp, cp, sp = (pad_rope_halves(t(a), dp).numpy() for a in (x, cos, sin))
     y = apply_rope_ref(x, cos, sin)

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(256) void pf_attn_bwd_delta_kernel(BwdParams p) {
 // dQ
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2)
+__global__ __launch_bounds__(256, (kWgPerCu<T, D>))
 void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
@@ -318,13 +318,26 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   using Frag = typename MF::Frag;
   using G = Tile<T, D>;
   // A step covers BMQ query rows of one head as NSUB sub-steps of 64 rows;
-  // 16-bit: 128 rows, so the per-step work (tile DMA issue, lse/delta
-  // staging, DMA wait, barrier) is shared by two sub-steps.
-  constexpr int BNK = 128, BMQ = sizeof(T) == 2 ? 128 : 64, NSUB = BMQ / 64;
-  constexpr bool kAcc = sizeof(T) == 2;  // dK/dV accumulators in AGPRs
+  // 16-bit up to head_dim 128: 128 rows, so the per-step work (tile DMA
+  // issue, lse/delta staging, DMA wait, barrier) is shared by two sub-steps,
+  // and the step runs as one fenced MFMA sequence with the dK/dV
+  // accumulators in AGPRs (kAcc). float32, and 16-bit at head_dim 256
+  // (whose 128-row double buffer would exceed the LDS and whose dK/dV
+  // accumulators alone fill the AGPRs): 64 rows with the plain step body.
+  constexpr bool kAcc = sizeof(T) == 2 && D <= 128;
+  constexpr int BNK = 128, BMQ = kAcc ? 128 : 64, NSUB = BMQ / 64;
   constexpr int KF = (D / 2) / MF::kK;
   constexpr int NDT = D / 32;
   constexpr int PF = 32 / MF::kK;
+  // dK/dV columns one workgroup accumulates: all D, or at head_dim 256 the
+  // 128-column half blockIdx.y selects (S and dP still contract over all D,
+  // so the two workgroups of a key block both compute them). The half's
+  // transposed reads are those of the first half 256 bytes further on: the
+  // tile swizzle permutes only the low 16 chunks (256 bytes) of a row.
+  constexpr int DA = D > 128 ? 128 : D, NDA = DA / 32;
+  static_assert(!kAcc || DA == D, "the fenced sequence accumulates every column");
+  static_assert(DA == D || (DA * (int)sizeof(T)) % 256 == 0, "column halves above the swizzled chunks");
+  const int dcol = DA == D ? 0 : (int)blockIdx.y * DA;
 
   // two buffers x (Q sub-tiles [NSUB], dO sub-tiles [NSUB], lse[BMQ], delta[BMQ])
   constexpr int BUF = 2 * NSUB * G::BYTES + 2 * BMQ * 4;
@@ -347,9 +360,9 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   load_row_frags<T, D>(static_cast<const T*>(p.k) + koff * D, kkey, kvalid, hh, kf);
   load_row_frags<T, D>(static_cast<const T*>(p.v) + koff * D, kkey, kvalid, hh, vf);
 
-  f32x16 dk[NDT], dv[NDT];
+  f32x16 dk[NDA], dv[NDA];
 #pragma unroll
-  for (int i = 0; i < NDT; ++i) {
+  for (int i = 0; i < NDA; ++i) {
     dk[i] = (f32x16)(0.f);
     dv[i] = (f32x16)(0.f);
   }
@@ -467,7 +480,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
                        int qb0) {
     constexpr int U = decltype(uc)::value;  // pass within the step
     f32x16 sx[2], dx[2];
-    if constexpr (sizeof(T) == 2) {
+    if constexpr (kAcc) {
       f32x4 lv[2][4], dl[2][4];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -683,8 +696,9 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
         Frag pfr[PF], dsf[PF];
         pack_frags<T>(sx[t], sx[t], pfr);
         pack_frags<T>(dx[t], dx[t], dsf);
-        mfma_trn<T, D, 2 * t, 2 * t + 2>(sdo, lane, ta, pfr, dv);
-        mfma_trn<T, D, 2 * t, 2 * t + 2>(sq, lane, ta, dsf, dk);
+        const int cb = dcol * (int)sizeof(T);  // byte offset of the column half
+        mfma_trn<T, D, 2 * t, 2 * t + 2, false, NDA>(sdo + cb, lane, ta, pfr, dv);
+        mfma_trn<T, D, 2 * t, 2 * t + 2, false, NDA>(sq + cb, lane, ta, dsf, dk);
       };
       half(std::integral_constant<int, 0>{});
       half(std::integral_constant<int, 1>{});
@@ -721,14 +735,14 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
 
   if constexpr (kAcc) {
 #pragma unroll
-    for (int i = 0; i < NDT; ++i) {
+    for (int i = 0; i < NDA; ++i) {
       agpr_fence(dk[i]);
       agpr_fence(dv[i]);
     }
   }
   if (kkey < p.Sk) {
-    store_acc_row<T, D>(static_cast<T*>(p.dk) + (koff + kkey) * D, dk, p.sm_scale, hh);
-    store_acc_row<T, D>(static_cast<T*>(p.dv) + (koff + kkey) * D, dv, 1.f, hh);
+    store_acc_row<T, DA>(static_cast<T*>(p.dk) + (koff + kkey) * D + dcol, dk, p.sm_scale, hh);
+    store_acc_row<T, DA>(static_cast<T*>(p.dv) + (koff + kkey) * D + dcol, dv, 1.f, hh);
   }
 }
 
@@ -757,7 +771,8 @@ hipError_t dq_typed(const BwdParams& p, bool causal, hipStream_t st) {
 template <typename T, int D>
 hipError_t dkv_typed(const BwdParams& p, bool causal, hipStream_t st) {
   const int n_kblk = (p.Sk + 127) / 128;
-  const dim3 grid(bwd_dkv_items(p));
+  // head_dim 256: two workgroups per key block, one per 128-column half of dK/dV
+  const dim3 grid(bwd_dkv_items(p), D > 128 ? 2 : 1);
   if (causal)
     hipLaunchKernelGGL((pf_attn_bwd_dkv_kernel<T, D, true>), grid, dim3(256), 0, st, p, n_kblk);
   else

@@ -51,7 +51,7 @@ constexpr int kFwdBN = 64;   // keys per block
 
 
 template <typename T, int D, bool CAUSAL, bool ROPE>
-__global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_attn_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(256, (kWgPerCu<T, D>)) void pf_attn_fwd_kernel(FwdParams p) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
   using G = Tile<T, D>;
@@ -590,6 +590,8 @@ template <typename T>
 hipError_t launch_dim(const FwdParams& p, int head_dim, bool causal, bool rope, hipStream_t st) {
   if (head_dim == 128) return launch_typed<T, 128>(p, causal, rope, st);
   if (head_dim == 64) return launch_typed<T, 64>(p, causal, rope, st);
+  if constexpr (sizeof(T) == 2)
+    if (head_dim == 256) return launch_typed<T, 256>(p, causal, rope, st);
   return hipErrorInvalidValue;
 }
 
@@ -624,6 +626,9 @@ hipError_t launch_rope_rotate_k(const void* k, void* k_out, const float* cos, co
     if (dtype == kF32) return rotate_typed<float, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
     if (dtype == kBF16) return rotate_typed<bf16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
     if (dtype == kF16) return rotate_typed<f16_t, 64>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
+  } else if (head_dim == 256) {
+    if (dtype == kBF16) return rotate_typed<bf16_t, 256>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
+    if (dtype == kF16) return rotate_typed<f16_t, 256>(k, k_out, cos, sin, B, Hkv, Sk, kv_len, inv, stream);
   }
   return hipErrorInvalidValue;
 }

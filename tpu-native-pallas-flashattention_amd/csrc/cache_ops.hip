@@ -9,9 +9,12 @@
 // (The single-token write of the fused decode step happens inside the
 // streaming decode kernel, decode_stream.hip.)
 //
-// Both kernels are bandwidth-trivial (a few rows per sequence): one thread
-// moves one 16-byte chunk of the first half of a row together with the chunk
-// D/2 further, so a row is 2 * D * ES / 16 coalesced 16-byte accesses.
+// Both kernels are bandwidth-trivial (a few rows per sequence): at the kernel
+// head dims (64, 128 and, 16-bit, 256) one thread moves one 16-byte chunk of
+// the first half of a row together with the chunk D/2 further, so a row is
+// 2 * D * ES / 16 coalesced 16-byte accesses; any other row of whole 16-byte
+// chunks (D = 0 instantiation: the row length p.dr read at run time) moves
+// one chunk per thread.
 // Positions come from device memory, so a caller can advance them on the
 // GPU between replays of a captured step.
 //
@@ -50,7 +53,8 @@ __device__ inline int64_t cache_slot(int64_t pos, int i, int seq_len, int cache_
 template <typename T, int D>
 __global__ __launch_bounds__(256) void pf_kv_cache_write_kernel(KvWriteParams p, int64_t n_items) {
   constexpr int EPC = 16 / (int)sizeof(T);
-  constexpr int HC = D / 2 / EPC;  // chunk pairs per row
+  const int dr = D > 0 ? D : p.dr;
+  const int HC = D > 0 ? D / 2 / EPC : p.dr / EPC;  // chunk pairs (D = 0: chunks) per row
   const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (item >= n_items) return;
   const int c = (int)(item % HC);
@@ -62,10 +66,10 @@ __global__ __launch_bounds__(256) void pf_kv_cache_write_kernel(KvWriteParams p,
   const int b = (int)(bh / p.Hkv);
   const int64_t slot = cache_slot(p.positions[(int64_t)b * p.pos_stride], i, p.L, p.C, p.ring != 0);
   if (slot < 0) return;
-  const T* src = static_cast<const T*>(which ? p.v : p.k) + (bh * p.L + i) * D + c * EPC;
-  T* dst = static_cast<T*>(which ? p.v_cache : p.k_cache) + (bh * p.C + slot) * D + c * EPC;
+  const T* src = static_cast<const T*>(which ? p.v : p.k) + (bh * p.L + i) * dr + c * EPC;
+  T* dst = static_cast<T*>(which ? p.v_cache : p.k_cache) + (bh * p.C + slot) * dr + c * EPC;
   stg16_nt(dst, ldg16_nt(src));
-  stg16_nt(dst + D / 2, ldg16_nt(src + D / 2));
+  if constexpr (D > 0) stg16_nt(dst + D / 2, ldg16_nt(src + D / 2));
 }
 
 // ---------------------------------------------------------------------------
@@ -74,7 +78,8 @@ __global__ __launch_bounds__(256) void pf_kv_cache_write_kernel(KvWriteParams p,
 template <typename T, int D>
 __global__ __launch_bounds__(256) void pf_paged_cache_write_kernel(PagedWriteParams p, int64_t n_items) {
   constexpr int EPC = 16 / (int)sizeof(T);
-  constexpr int HC = D / 2 / EPC;
+  const int dr = D > 0 ? D : p.dr;
+  const int HC = D > 0 ? D / 2 / EPC : p.dr / EPC;
   const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (item >= n_items) return;
   const int c = (int)(item % HC);
@@ -91,16 +96,16 @@ __global__ __launch_bounds__(256) void pf_paged_cache_write_kernel(PagedWritePar
   const int page = p.block_tables[(int64_t)b * p.pages_per_seq + lp];
   if (page < 0 || page >= p.num_pages) return;
   const int off = (int)(pos - lp * p.page_size);
-  const T* src = static_cast<const T*>(which ? p.v : p.k) + (bh * p.L + i) * D + c * EPC;
+  const T* src = static_cast<const T*>(which ? p.v : p.k) + (bh * p.L + i) * dr + c * EPC;
   T* dst = static_cast<T*>(which ? p.v_pages : p.k_pages) +
-           (((int64_t)page * p.Hkv + kvh) * p.page_size + off) * D + c * EPC;
+           (((int64_t)page * p.Hkv + kvh) * p.page_size + off) * dr + c * EPC;
   stg16_nt(dst, ldg16_nt(src));
-  stg16_nt(dst + D / 2, ldg16_nt(src + D / 2));
+  if constexpr (D > 0) stg16_nt(dst + D / 2, ldg16_nt(src + D / 2));
 }
 
 template <typename T, int D>
 hipError_t kv_write_typed(const KvWriteParams& p, hipStream_t st) {
-  constexpr int HC = D / 2 / (16 / (int)sizeof(T));
+  const int HC = D > 0 ? D / 2 / (16 / (int)sizeof(T)) : p.dr / (16 / (int)sizeof(T));
   const int64_t n = (int64_t)p.B * p.Hkv * 2 * p.L * HC;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL((pf_kv_cache_write_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, n);
@@ -109,7 +114,7 @@ hipError_t kv_write_typed(const KvWriteParams& p, hipStream_t st) {
 
 template <typename T, int D>
 hipError_t paged_write_typed(const PagedWriteParams& p, hipStream_t st) {
-  constexpr int HC = D / 2 / (16 / (int)sizeof(T));
+  const int HC = D > 0 ? D / 2 / (16 / (int)sizeof(T)) : p.dr / (16 / (int)sizeof(T));
   const int64_t n = (int64_t)p.B * p.Hkv * 2 * p.L * HC;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL((pf_paged_cache_write_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
@@ -127,6 +132,13 @@ hipError_t paged_write_typed(const PagedWriteParams& p, hipStream_t st) {
       if (dtype == kF32) return FN<float, 64>(__VA_ARGS__);        \
       if (dtype == kBF16) return FN<bf16_t, 64>(__VA_ARGS__);      \
       if (dtype == kF16) return FN<f16_t, 64>(__VA_ARGS__);        \
+    } else if (head_dim == 256 && dtype != kF32) {                 \
+      if (dtype == kBF16) return FN<bf16_t, 256>(__VA_ARGS__);     \
+      if (dtype == kF16) return FN<f16_t, 256>(__VA_ARGS__);       \
+    } else {                                                       \
+      if (dtype == kF32) return FN<float, 0>(__VA_ARGS__);         \
+      if (dtype == kBF16) return FN<bf16_t, 0>(__VA_ARGS__);       \
+      if (dtype == kF16) return FN<f16_t, 0>(__VA_ARGS__);         \
     }                                                              \
     return hipErrorInvalidValue;                                   \
   } while (0)

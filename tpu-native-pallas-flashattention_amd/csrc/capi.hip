@@ -44,17 +44,21 @@ Tuning& tuning() {
 }
 
 bool dtype_ok(int32_t d) { return d == PF_DTYPE_F32 || d == PF_DTYPE_BF16 || d == PF_DTYPE_F16; }
-bool head_dim_ok(int32_t d) { return d == 64 || d == 128; }
+// Kernel head dims: 64 and 128 for every dtype, 256 for bf16/f16 (a float32
+// tile of 256 columns would not fit the LDS double buffers). dtype must
+// already be valid.
+int32_t max_head_dim(int32_t dtype) { return dtype == PF_DTYPE_F32 ? 128 : 256; }
+bool head_dim_ok(int32_t d, int32_t dtype) { return d == 64 || d == 128 || (d == 256 && d <= max_head_dim(dtype)); }
 
-// Decode and paged decode also read rows of any head_dim up to 128 that are
-// whole 16-byte chunks (a multiple of 8 elements for bf16/f16, 4 for float32)
-// in place: the generic kernel computes at 64 or 128 with the missing columns
-// as zeros. dtype must already be valid.
+// Decode and paged decode also read rows of any head_dim up to the dtype's
+// maximum that are whole 16-byte chunks (a multiple of 8 elements for
+// bf16/f16, 4 for float32) in place: the generic kernel computes at the next
+// kernel head dim with the missing columns as zeros.
 bool decode_head_dim_ok(int32_t d, int32_t dtype) {
   const int32_t es = dtype == PF_DTYPE_F32 ? 4 : 2;
-  return d >= 1 && d <= 128 && (d * es) % 16 == 0;
+  return d >= 1 && d <= max_head_dim(dtype) && (d * es) % 16 == 0;
 }
-int32_t decode_compute_dim(int32_t d) { return d <= 64 ? 64 : 128; }
+int32_t decode_compute_dim(int32_t d) { return d <= 64 ? 64 : d <= 128 ? 128 : 256; }
 
 constexpr int64_t kMaxGrid = 0x7fffffff;
 
@@ -66,7 +70,7 @@ int check_attn_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk, 
   if (kv_len < 1 || kv_len > Sk) return PF_ERR_INVALID;
   if (!isfinite(scale)) return PF_ERR_INVALID;
   if (!dtype_ok(dtype)) return PF_ERR_UNSUPPORTED;
-  if (!head_dim_ok(D)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(D, dtype)) return PF_ERR_UNSUPPORTED;
   return PF_OK;
 }
 
@@ -551,7 +555,7 @@ int pf_rope(const pf_rope_args* a, void* stream) {
     return PF_ERR_INVALID;
   if (a->inverse != 0 && a->inverse != 1) return PF_ERR_INVALID;
   if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
-  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if (!head_dim_ok(a->head_dim, a->dtype)) return PF_ERR_UNSUPPORTED;
   if ((int64_t)a->batch * a->heads * a->seq_len == 0) return PF_OK;
   if (!a->x || !a->out || !a->cos || !a->sin || a->rope_len < a->seq_len) return PF_ERR_INVALID;
   return finish(pf::launch_rope_rotate_k(a->x, a->out, a->cos, a->sin, a->batch, a->heads, a->seq_len,
@@ -568,11 +572,11 @@ int pf_kv_cache_write(const pf_kv_cache_write_args* a, void* stream) {
   if (a->positions_stride != 0 && a->positions_stride != 1) return PF_ERR_INVALID;
   if (a->ring != 0 && a->ring != 1) return PF_ERR_INVALID;
   if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
-  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if (!decode_head_dim_ok(a->head_dim, a->dtype)) return PF_ERR_UNSUPPORTED;
   if ((int64_t)a->batch * a->num_kv_heads * a->seq_len == 0) return PF_OK;
   if (!a->k || !a->v || !a->k_cache || !a->v_cache || !a->positions) return PF_ERR_INVALID;
   pf::KvWriteParams p{a->k, a->v, a->k_cache, a->v_cache, a->positions, a->positions_stride,
-                      a->batch, a->num_kv_heads, a->seq_len, a->cache_size, a->ring};
+                      a->batch, a->num_kv_heads, a->seq_len, a->cache_size, a->ring, a->head_dim};
   return finish(pf::launch_kv_cache_write(p, a->dtype, a->head_dim, (hipStream_t)stream));
 }
 
@@ -583,12 +587,12 @@ int pf_paged_cache_write(const pf_paged_cache_write_args* a, void* stream) {
     return PF_ERR_INVALID;
   if (a->positions_stride != 0 && a->positions_stride != 1) return PF_ERR_INVALID;
   if (!dtype_ok(a->dtype)) return PF_ERR_UNSUPPORTED;
-  if (!head_dim_ok(a->head_dim)) return PF_ERR_UNSUPPORTED;
+  if (!decode_head_dim_ok(a->head_dim, a->dtype)) return PF_ERR_UNSUPPORTED;
   if ((int64_t)a->batch * a->num_kv_heads * a->seq_len == 0 || a->pages_per_seq == 0) return PF_OK;
   if (!a->k || !a->v || !a->k_pages || !a->v_pages || !a->positions || !a->block_tables) return PF_ERR_INVALID;
   pf::PagedWriteParams p{a->k, a->v, a->k_pages, a->v_pages, a->block_tables, a->positions,
                          a->positions_stride, a->batch, a->num_kv_heads, a->seq_len, a->num_pages,
-                         a->page_size, a->pages_per_seq};
+                         a->page_size, a->pages_per_seq, a->head_dim};
   return finish(pf::launch_paged_cache_write(p, a->dtype, a->head_dim, (hipStream_t)stream));
 }
 

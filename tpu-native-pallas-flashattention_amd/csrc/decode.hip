@@ -53,7 +53,7 @@ __device__ inline const T* key_row(const DecodeParams& p, const T* base, int b, 
 }
 
 template <typename T, int D, bool PAGED>
-__global__ __launch_bounds__(256, (sizeof(T) == 4 && D == 128) ? 1 : 2) void pf_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, (kWgPerCu<T, D>)) void pf_decode_kernel(DecodeParams p) {
   using MF = Mfma32<T>;
   using Frag = typename MF::Frag;
   constexpr int BN = kDecBN;
@@ -338,6 +338,9 @@ template <typename T, bool PAGED>
 hipError_t launch_dim(const DecodeParams& p, bool combine, hipStream_t st) {
   if (p.D == 128) return combine ? launch_combine_typed<T, 128, PAGED>(p, st) : launch_typed<T, 128, PAGED>(p, st);
   if (p.D == 64) return combine ? launch_combine_typed<T, 64, PAGED>(p, st) : launch_typed<T, 64, PAGED>(p, st);
+  if constexpr (sizeof(T) == 2)
+    if (p.D == 256)
+      return combine ? launch_combine_typed<T, 256, PAGED>(p, st) : launch_typed<T, 256, PAGED>(p, st);
   return hipErrorInvalidValue;
 }
 

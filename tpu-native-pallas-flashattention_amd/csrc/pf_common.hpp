@@ -102,6 +102,13 @@ constexpr int frags_per_chunk() {
   return 16 / (Mfma32<T>::kK * (int)sizeof(T));
 }
 
+// Workgroups per CU the 256-thread prefill and decode kernels are built for
+// (the second __launch_bounds__ argument): 1 where a wave needs more than
+// 256 registers (float32 at head_dim 128, every type at head_dim 256) or a
+// workgroup more than half the LDS, else 2.
+template <typename T, int D>
+inline constexpr int kWgPerCu = ((sizeof(T) == 4 && D == 128) || D > 128) ? 1 : 2;
+
 // Reinterpret a 16-byte chunk as operand fragment i.
 template <typename T>
 __device__ inline typename Mfma32<T>::Frag chunk_frag(const u32x4& c, int i) {

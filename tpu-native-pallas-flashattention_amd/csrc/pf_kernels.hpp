@@ -234,6 +234,7 @@ struct KvWriteParams {
   int pos_stride;
   int B, Hkv, L, C;
   int ring;  // 0: slot pos + i; 1: slot (pos + i) % C, last C rows only
+  int dr;    // row length in elements (the head_dim; whole 16-byte chunks)
 };
 hipError_t launch_kv_cache_write(const KvWriteParams& p, int dtype, int head_dim, hipStream_t stream);
 
@@ -246,6 +247,7 @@ struct PagedWriteParams {
   const int32_t* positions;
   int pos_stride;
   int B, Hkv, L, num_pages, page_size, pages_per_seq;
+  int dr;  // row length in elements (the head_dim; whole 16-byte chunks)
 };
 hipError_t launch_paged_cache_write(const PagedWriteParams& p, int dtype, int head_dim, hipStream_t stream);
 

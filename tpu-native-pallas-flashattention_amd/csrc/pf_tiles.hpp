@@ -217,10 +217,13 @@ __device__ inline void agpr_fence(f32x16& acc) { asm volatile("s_nop 7\n\ts_nop 
 // for step c are tile rows 32hh + 8c + [0, 8) (16-bit) or 32hh + s (f32).
 // Steps [C0, C1) of 4 (16-bit: step c = tile rows 32hh + 8c + [0, 8); f32:
 // rows 32hh + 8c .. 32hh + 8c + 7 as 8 single-row steps); bf is indexed by step.
-// AGPR = true (16-bit T only): accumulate with MfmaAgpr.
-template <typename T, int D, int C0 = 0, int C1 = 4, bool AGPR = false>
+// AGPR = true (16-bit T only): accumulate with MfmaAgpr. NA: the column
+// blocks accumulated, the first NA of the tile (16-bit T may pass a tile
+// pointer moved on by a multiple of 256 bytes for a later range of columns).
+template <typename T, int D, int C0 = 0, int C1 = 4, bool AGPR = false, int NA = D / 32>
 __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& ta,
                                 const typename Mfma32<T>::Frag* bf, f32x16* acc) {
+  static_assert(NA >= 1 && NA <= D / 32, "column blocks of the tile");
   using MF = Mfma32<T>;
   using G = Tile<T, D>;
   using Frag = typename MF::Frag;
@@ -231,7 +234,7 @@ __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& 
 #pragma unroll
     for (int c = C0; c < C1; ++c)
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
+      for (int dt = 0; dt < NA; ++dt) {
         v4i16 part[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r)
@@ -247,7 +250,7 @@ __device__ inline void mfma_trn(const char* tile, int lane, const TrAddr<T, D>& 
     for (int s = 8 * C0; s < 8 * C1; ++s) {
       const int row = 32 * hh + s;
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
+      for (int dt = 0; dt < NA; ++dt) {
         const int d = 32 * dt + l32;
         const float a = *reinterpret_cast<const float*>(
             tile + row * G::RB + 16 * ((d >> 2) ^ tile_swz<G::CPR>(row)) + 4 * (d & 3));

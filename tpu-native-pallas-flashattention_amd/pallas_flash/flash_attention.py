@@ -20,9 +20,11 @@ reached through the C ABI in ``include/pallas_flash_amd.h``.
 
 ``block_q``/``block_k`` are accepted for signature compatibility; tile shapes
 are chosen by the kernels. ``interpret`` is accepted and ignored: there is no
-CPU interpreter here, the HIP kernels always run. Any head_dim up to 128 and
-any mix of input dtypes are accepted (``_shape``: zero-padding to the kernels'
-head_dim, float32 compute for mixed dtypes, output in q's dtype).
+CPU interpreter here, the HIP kernels always run. Any head_dim up to 256
+(bfloat16/float16) or 128 (float32 compute, which mixed dtypes use) and any
+mix of input dtypes are accepted (``_shape``: zero-padding to the kernels'
+head_dim 64, 128 or 256, float32 compute for mixed dtypes, output in q's
+dtype).
 """
 
 from __future__ import annotations
@@ -147,7 +149,8 @@ def flash_attention(
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
     _lib.require_device(q, k, v)
-    cdt, dp = compute_dtype(q, k, v), kernel_head_dim(head_dim)
+    cdt = compute_dtype(q, k, v)
+    dp = kernel_head_dim(head_dim, cdt)
     q2, k2, v2 = (adapt(x, cdt, dp).contiguous() for x in (q, k, v))
     o = _FlashAttentionFn.apply(q2, k2, v2, bool(causal), float(sm_scale), kv_len)
     return restore(o, head_dim, q.dtype)
@@ -162,7 +165,8 @@ def flash_attention_with_lse(q, k, v, *, causal=False, sm_scale=None, kv_len=Non
     if sm_scale is None:
         sm_scale = 1.0 / (head_dim ** 0.5)
     _lib.require_device(q, k, v)
-    cdt, dp = compute_dtype(q, k, v), kernel_head_dim(head_dim)
+    cdt = compute_dtype(q, k, v)
+    dp = kernel_head_dim(head_dim, cdt)
     q2, k2, v2 = (adapt(x, cdt, dp).contiguous() for x in (q, k, v))
     o, lse = _fwd(q2, k2, v2, bool(causal), float(sm_scale), kv_len, True)
     return restore(o, head_dim, q.dtype), lse

@@ -21,8 +21,9 @@ Numerics: the rotated Q and K are rounded once to the input dtype before the
 bf16/f16 MFMA (the reference keeps them in float32 and runs a float32 dot,
 fused_rope.py:75-78); float32 inputs keep float32 throughout.
 
-head_dim below 128 other than 64 is zero-padded half by half (each element
-keeps its rotation partner) and mixed dtypes compute in float32 (``_shape``).
+A head_dim that is not a kernel size (64, 128, or 256 for bfloat16/float16)
+is zero-padded half by half to the next one (each element keeps its rotation
+partner) and mixed dtypes compute in float32 (``_shape``).
 """
 
 from __future__ import annotations
@@ -155,7 +156,8 @@ def flash_attention_rope(
         raise ValueError(f"kv_len must be in (0, {seq_len_k}], got {kv_len}")
     _lib.require_device(q, k, v)
     dev = q.device
-    cdt, dp = compute_dtype(q, k, v), kernel_head_dim(head_dim)
+    cdt = compute_dtype(q, k, v)
+    dp = kernel_head_dim(head_dim, cdt)
     tables = [pad_rope_halves(_table(t, dev), dp).contiguous() for t in (q_cos, q_sin, k_cos, k_sin)]
     o = _RopeFn.apply(pad_rope_halves(q.to(cdt), dp).contiguous(), pad_rope_halves(k.to(cdt), dp).contiguous(),
                       pad_head_dim(v.to(cdt), dp).contiguous(), *tables, bool(causal), float(sm_scale),

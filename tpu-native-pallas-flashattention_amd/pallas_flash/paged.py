@@ -50,9 +50,10 @@ def paged_flash_attention(
 
     Returns:
         ``[batch, num_heads, 1, head_dim]`` in q's dtype. Any head_dim up to
-        128 that is a multiple of 8 (bfloat16/float16) or 4 (float32) is read
-        in place; other head dims and mixed dtypes copy the pool padded/cast
-        per call, with a one-time warning (``_shape``).
+        256 that is a multiple of 8 (bfloat16/float16), or up to 128 that is
+        a multiple of 4 (float32), is read in place; other head dims and
+        mixed dtypes copy the pool padded/cast per call, with a one-time
+        warning (``_shape``).
     """
     # paged.py:129-149
     if q.dim() != 4 or q.shape[2] != 1:
