@@ -135,6 +135,37 @@ def test_write_to_paged_cache_reference_signature():
     assert np.array_equal(_bits(kp), want)
 
 
+@pytest.mark.parametrize("which", ["paged", "contiguous"])
+def test_cache_writes_out_of_place(which):
+    """inplace=False: the given cache or pool is left bit-identical and the
+    returned copies hold exactly what the in-place write produces (the
+    reference's functional update, paged.py:205-223 / model.py:257-262)."""
+    note(f"cache write out of place: {which}")
+    rng = np.random.default_rng(15)
+    if which == "paged":
+        kp = dev(rng.standard_normal((6, 2, 16, 128)), "bf16")
+        vp = dev(rng.standard_normal((6, 2, 16, 128)), "bf16")
+        k = dev(rng.standard_normal((2, 2, 3, 128)), "bf16")
+        table = torch.tensor([[4, 1, -1], [0, 5, 2]], dtype=torch.int32)
+        pos = torch.tensor([14, 20], dtype=torch.int32, device=DEV)
+        call = lambda a, b, inplace: write_to_paged_cache(a, b, k, k, table, pos, inplace=inplace)
+    else:
+        kp = dev(rng.standard_normal((2, 2, 16, 96)), "f16")
+        vp = dev(rng.standard_normal((2, 2, 16, 96)), "f16")
+        k = dev(rng.standard_normal((2, 2, 5, 96)), "f16")
+        call = lambda a, b, inplace: write_kv_cache(a, b, k, k, [3, 13], ring=True, inplace=inplace)
+    before_k, before_v = _bits(kp), _bits(vp)
+    nk, nv = call(kp, vp, False)
+    torch.cuda.synchronize()
+    assert nk.data_ptr() != kp.data_ptr() and nv.data_ptr() != vp.data_ptr()
+    assert np.array_equal(_bits(kp), before_k) and np.array_equal(_bits(vp), before_v)
+    assert not np.array_equal(_bits(nk), before_k)
+    ik, iv = call(kp, vp, True)
+    torch.cuda.synchronize()
+    assert ik is kp and iv is vp
+    assert np.array_equal(_bits(nk), _bits(kp)) and np.array_equal(_bits(nv), _bits(vp))
+
+
 # -------------------------------------------------------------- decode step --
 def _step_inputs(rng, B, Hq, Hkv, C, D, dt):
     return (dev(rng.standard_normal((B, Hq, 1, D)), dt), dev(rng.standard_normal((B, Hkv, 1, D)), dt),

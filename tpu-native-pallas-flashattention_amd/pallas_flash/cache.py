@@ -55,8 +55,8 @@ def _positions(positions, batch: int, device) -> Tuple[torch.Tensor, int]:
 
 
 def write_kv_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                   positions, *, ring: bool = False):
-    """Write rows of ``k``/``v`` into a contiguous KV cache in place.
+                   positions, *, ring: bool = False, inplace: bool = True):
+    """Write rows of ``k``/``v`` into a contiguous KV cache (in place by default).
 
     ``_cache_write`` (model.py:257-262) for ``ring=False``: row ``i`` of batch
     ``b`` goes to slot ``positions[b] + i``; rows past the capacity are not
@@ -69,8 +69,12 @@ def write_kv_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor
         k, v: ``[batch, num_kv_heads, seq_len, head_dim]`` (cast to the cache dtype).
         positions: absolute position of row 0: an int, or ``[batch]`` integers
             (a device tensor keeps the call free of host-side data).
+        inplace: ``True`` writes into ``k_cache``/``v_cache`` and returns
+            them; ``False`` leaves them unchanged and returns written copies,
+            as the reference's functional ``dynamic_update_slice`` does (one
+            cache-sized device copy per call).
 
-    Returns ``(k_cache, v_cache)``.
+    Returns ``(k_cache, v_cache)``: the given tensors, or the new ones.
     """
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
         raise ValueError("k_cache and v_cache must be [batch, num_kv_heads, capacity, head_dim] of one shape")
@@ -83,6 +87,8 @@ def write_kv_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor
         raise ValueError("k_cache and v_cache must share a dtype")
     _check_positions(positions, batch)
     _lib.require_device(k_cache, v_cache, k, v)
+    if not inplace:
+        k_cache, v_cache = (t.clone(memory_format=torch.contiguous_format) for t in (k_cache, v_cache))
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("the caches are written in place and must be contiguous")
     dev = k_cache.device

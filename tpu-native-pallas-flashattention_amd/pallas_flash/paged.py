@@ -115,9 +115,9 @@ def init_paged_cache(num_pages: int, num_kv_heads: int, page_size: int, head_dim
             torch.zeros(shape, dtype=dtype, device=device))
 
 
-def write_to_paged_cache(k_pages, v_pages, k, v, block_table, position):
+def write_to_paged_cache(k_pages, v_pages, k, v, block_table, position, *, inplace: bool = True):
     """Write token K/V into the pages holding their positions
-    (paged.py:205-223), on device (pf_paged_cache_write), in place.
+    (paged.py:205-223), on device (pf_paged_cache_write), in place by default.
 
     The reference writes one token of one sequence: ``k``/``v``
     ``[1, num_kv_heads, 1, head_dim]``, ``block_table`` ``[pages_per_seq]``,
@@ -130,8 +130,13 @@ def write_to_paged_cache(k_pages, v_pages, k, v, block_table, position):
     written (the reference's dynamic_update_slice would clamp it onto a valid
     slot).
 
-    Returns the updated ``(k_pages, v_pages)`` (the same tensors), so the
-    reference's functional call pattern keeps working.
+    Returns the updated ``(k_pages, v_pages)``: with ``inplace=True``
+    (default) the same tensors, written in place, so the reference's
+    functional call pattern keeps working without a pool copy; with
+    ``inplace=False`` written copies, the given pools left unchanged, as the
+    reference's functional update leaves them (one pool-sized device copy
+    per call: for callers that keep the pre-write pool, e.g. to roll back
+    speculative tokens).
     """
     from .cache import _check_positions, _positions
     if k_pages.dim() != 4 or k_pages.shape != v_pages.shape:
@@ -151,6 +156,8 @@ def write_to_paged_cache(k_pages, v_pages, k, v, block_table, position):
         raise ValueError(f"block_table must be [pages_per_seq] or [batch, pages_per_seq], got {tuple(table.shape)}")
     _check_positions(position, batch)
     _lib.require_device(k_pages, v_pages, k, v)
+    if not inplace:
+        k_pages, v_pages = (t.clone(memory_format=torch.contiguous_format) for t in (k_pages, v_pages))
     if not (k_pages.is_contiguous() and v_pages.is_contiguous()):
         raise ValueError("the page pools are written in place and must be contiguous")
     dev = k_pages.device
