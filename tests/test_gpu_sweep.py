@@ -5,6 +5,8 @@ The fixed-shape tests re-express the reference's own cases; this sweep adds
 the combinations they leave out: every dtype with both head dims, GQA ratios
 1 to 8, Sq and Sk from below one tile to a few tiles (independently, so
 Sq != Sk with top-left causal masking), kv_len < Sk and a non-default scale.
+A second, smaller set per test draws the same way at head_dim 256
+(bfloat16/float16, the dtypes that have it).
 """
 
 from __future__ import annotations
@@ -39,6 +41,18 @@ def _cases(seed: int):
     return cases
 
 
+def _wide(cases, seed: int, n: int, tag: str):
+    """n cases drawn like `cases`' generator but at head_dim 256, 16-bit dtypes:
+    the parameters of n of them with D and dt replaced."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i, c in enumerate(rng.choice(len(cases), size=n, replace=False)):
+        v = list(cases[c].values)
+        v[0], v[1] = ("bf16", "f16")[i % 2], 256
+        out.append(pytest.param(*v, id=f"{tag}{i}-{v[0]}-D256"))
+    return out
+
+
 def _inputs(seed, dt, B, Hq, Hkv, Sq, Sk, D):
     rng = np.random.default_rng(seed)
     q = dev(rng.standard_normal((B, Hq, Sq, D)), dt)
@@ -48,7 +62,7 @@ def _inputs(seed, dt, B, Hq, Hkv, Sq, Sk, D):
     return q, k, v, do
 
 
-@pytest.mark.parametrize("dt,D,B,Hq,Hkv,Sq,Sk,causal,kv_len,scale", _cases(101))
+@pytest.mark.parametrize("dt,D,B,Hq,Hkv,Sq,Sk,causal,kv_len,scale", _cases(101) + _wide(_cases(101), 505, 6, "w"))
 def test_sweep_forward_and_lse(dt, D, B, Hq, Hkv, Sq, Sk, causal, kv_len, scale):
     note(f"sweep fwd dt={dt} D={D} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Sk={Sk} causal={causal} "
          f"kv_len={kv_len} scale={scale}")
@@ -61,7 +75,7 @@ def test_sweep_forward_and_lse(dt, D, B, Hq, Hkv, Sq, Sk, causal, kv_len, scale)
     assert lse_err <= (1e-5 if dt == "f32" else 1e-3), f"lse error {lse_err:.3e}"
 
 
-@pytest.mark.parametrize("dt,D,B,Hq,Hkv,Sq,Sk,causal,kv_len,scale", _cases(202))
+@pytest.mark.parametrize("dt,D,B,Hq,Hkv,Sq,Sk,causal,kv_len,scale", _cases(202) + _wide(_cases(202), 606, 6, "w"))
 def test_sweep_backward(dt, D, B, Hq, Hkv, Sq, Sk, causal, kv_len, scale):
     note(f"sweep bwd dt={dt} D={D} B={B} Hq={Hq} Hkv={Hkv} Sq={Sq} Sk={Sk} causal={causal} "
          f"kv_len={kv_len} scale={scale}")
@@ -93,7 +107,8 @@ def _rope_cases(seed: int, n: int):
     return cases
 
 
-@pytest.mark.parametrize("dt,D,Hq,Hkv,Sq,Sk,causal,kv_len", _rope_cases(303, 12))
+@pytest.mark.parametrize("dt,D,Hq,Hkv,Sq,Sk,causal,kv_len",
+                         _rope_cases(303, 12) + _wide(_rope_cases(303, 12), 707, 4, "rw"))
 def test_sweep_rope_forward_backward(dt, D, Hq, Hkv, Sq, Sk, causal, kv_len):
     """Fused RoPE (separate K tables when Sq != Sk, fused_rope.py:154-160)
     forward and its RoPE-aware backward vs the oracle."""
@@ -130,7 +145,7 @@ def _decode_cases(seed: int, n: int):
     return cases
 
 
-@pytest.mark.parametrize("dt,D,B,Hq,Hkv,cap,L", _decode_cases(404, 12))
+@pytest.mark.parametrize("dt,D,B,Hq,Hkv,cap,L", _decode_cases(404, 12) + _wide(_decode_cases(404, 12), 808, 4, "dw"))
 def test_sweep_decode(dt, D, B, Hq, Hkv, cap, L):
     """Decode over the [0, L) prefix of a cache of `cap` slots whose tail is
     NaN (test_decode.py:33, :38-49)."""
@@ -148,17 +163,20 @@ def test_sweep_decode(dt, D, B, Hq, Hkv, cap, L):
     check_fwd(out, decode_ref(host(tq), host(tk), host(tv), L), dt)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(12))
 def test_sweep_paged(seed):
     """Paged decode over scrambled, partly shared pages with -1 padding past
     each sequence's last page and NaN everywhere no valid row lives
-    (paged.py:119-121; test_paged.py:25-28, :61-91)."""
+    (paged.py:119-121; test_paged.py:25-28, :61-91). Seeds 8-11: head_dim 256."""
     from oracle import paged_ref
     from pallas_flash import paged_flash_attention
     import torch
     rng = np.random.default_rng(500 + seed)
-    dt = ("bf16", "f16", "f32")[seed % 3]
-    D = (128, 64)[(seed // 3) % 2]
+    if seed < 8:
+        dt = ("bf16", "f16", "f32")[seed % 3]
+        D = (128, 64)[(seed // 3) % 2]
+    else:
+        dt, D = ("bf16", "f16")[seed % 2], 256
     Hkv = int(rng.integers(1, 4))
     Hq = Hkv * int(rng.choice([1, 2, 4, 8]))
     page = int(rng.choice([16, 32, 64, 128]))
