@@ -163,8 +163,13 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
   int n_plain = (q0 + BM > p.Sq) ? 0 : min(nblk, p.kv_len / BN);
   if constexpr (CAUSAL) n_plain = min(n_plain, q0 / BN);
 
+  // Valid keys of this lane's query: key < klim (kv_len, and causal key <= q).
+  const int klim = qvalid ? (CAUSAL ? min(p.kv_len, qrow + 1) : p.kv_len) : 0;
   auto block = [&](auto masked, int j) {
     const int kv0 = j * BN;
+    // masked blocks: bit 16t + r says whether key kv0 + 32hh + 16t + r is valid
+    uint32_t vmask = 0u;
+    if constexpr (decltype(masked)::value) vmask = bit_range(0, klim - kv0 - 32 * hh);
     const char* sk = smem + (j & 1) * (2 * G::BYTES);
     const char* sv = sk + G::BYTES;
     if (j + 1 < nblk) {
@@ -196,11 +201,7 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
       auto pds = [&](auto tc, int r) __attribute__((always_inline)) {
         constexpr int t = decltype(tc)::value;
         float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lse2));
-        if constexpr (decltype(masked)::value) {
-          const int key = kv0 + 32 * hh + 16 * t + r;
-          const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
-          pv = ok ? pv : 0.f;
-        }
+        if constexpr (decltype(masked)::value) pv = keep_if_bit(pv, vmask, 16 * t + r);
         sx[t][r] = pv * dx[t][r];
         if (r & 1) dw[t][r >> 1] = pack2<T>(sx[t][r - 1], sx[t][r]);
       };
@@ -285,11 +286,7 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float pv = __builtin_amdgcn_exp2f(fmaf(sx[r], p.scale_log2, -lse2));
-        if constexpr (decltype(masked)::value) {
-          const int key = kv0 + 32 * hh + 16 * t + r;
-          const bool ok = qvalid && key < p.kv_len && (!CAUSAL || key <= qrow);
-          pv = ok ? pv : 0.f;
-        }
+        if constexpr (decltype(masked)::value) pv = keep_if_bit(pv, vmask, 16 * t + r);
         sx[r] = pv * (dx[r] - dlt);
       }
       // pack_frags(x, x) puts this half's fragments in both slot ranges;
@@ -479,6 +476,14 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
   auto step_body = [&](auto masked, auto uc, const char* sq, const char* sdo, const float* slse, const float* sdl,
                        int qb0) {
     constexpr int U = decltype(uc)::value;  // pass within the step
+    // Masked steps: value (half t, register r) of this lane is query
+    // qb0 + 32hh + 16t + r against key kkey; bit 16t + r of vmask says whether
+    // it is valid (key < kv_len, query < Sq, causal key <= query).
+    uint32_t vmask = 0u;
+    if constexpr (decltype(masked)::value) {
+      const int base = qb0 + 32 * hh;
+      vmask = kvalid ? bit_range(CAUSAL ? kkey - base : 0, p.Sq - base) : 0u;
+    }
     f32x16 sx[2], dx[2];
     if constexpr (kAcc) {
       f32x4 lv[2][4], dl[2][4];
@@ -498,11 +503,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       auto pds = [&](auto tc, int r) {
         constexpr int t = decltype(tc)::value;
         float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lv[t][r >> 2][r & 3]));
-        if constexpr (decltype(masked)::value) {
-          const int q = qb0 + 32 * hh + 16 * t + r;
-          const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
-          pv = ok ? pv : 0.f;
-        }
+        if constexpr (decltype(masked)::value) pv = keep_if_bit(pv, vmask, 16 * t + r);
         const float ds = pv * dx[t][r];
         sx[t][r] = pv;
         dx[t][r] = ds;
@@ -531,11 +532,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           asm volatile("" : "+v"(ya[t][r]));
         } else if constexpr (st == 1) {
           float pv = __builtin_amdgcn_exp2f(ya[t][r]);
-          if constexpr (decltype(masked)::value) {
-            const int q = qb0 + 32 * hh + 16 * t + r;
-            const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
-            pv = ok ? pv : 0.f;
-          }
+          if constexpr (decltype(masked)::value) pv = keep_if_bit(pv, vmask, 16 * t + r);
           pe[t][r] = pv;
           asm volatile("" : "+v"(pe[t][r]));
         } else {
@@ -682,11 +679,7 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * r4 + e;
             float pv = __builtin_amdgcn_exp2f(fmaf(sx[t][r], p.scale_log2, -lv[e]));
-            if constexpr (decltype(masked)::value) {
-              const int q = qb0 + 32 * hh + 16 * t + r;
-              const bool ok = kvalid && q < p.Sq && (!CAUSAL || kkey <= q);
-              pv = ok ? pv : 0.f;
-            }
+            if constexpr (decltype(masked)::value) pv = keep_if_bit(pv, vmask, 16 * t + r);
             dx[t][r] = pv * (dx[t][r] + dl[e]);  // dl = -delta
             sx[t][r] = pv;
           }

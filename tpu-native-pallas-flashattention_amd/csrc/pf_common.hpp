@@ -102,6 +102,28 @@ constexpr int frags_per_chunk() {
   return 16 / (Mfma32<T>::kK * (int)sizeof(T));
 }
 
+// Bits [lo, hi) of a 32-bit word, lo and hi clamped to [0, 32] (0 when the
+// range is empty): the valid values of a lane's 32 scores in one step.
+__device__ inline uint32_t bit_range(int lo, int hi) {
+  lo = lo < 0 ? 0 : lo;
+  hi = hi > 32 ? 32 : hi;
+  if (hi <= lo) return 0u;
+  const uint32_t top = hi >= 32 ? 0xffffffffu : (1u << hi) - 1u;
+  return top & ~((1u << lo) - 1u);
+}
+
+// v where bit i of m is set, +0.0 where it is clear. Bitwise (bit i
+// sign-extended over the word by v_bfe_i32, then AND): two VALU operations
+// and no branch, and a masked value that overflowed to inf still becomes
+// exactly 0. The extract is written as assembly because the compiler
+// rewrites a one-bit sign extension into AND + compare + select (three).
+// i must be a constant once the caller's loops are unrolled (0..31).
+__device__ inline float keep_if_bit(float v, uint32_t m, int i) {
+  uint32_t sel;
+  asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(sel) : "v"(m), "i"(i));
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & sel);
+}
+
 // Workgroups per CU the 256-thread prefill and decode kernels are built for
 // (the second __launch_bounds__ argument): 1 where a wave needs more than
 // 256 registers (float32 at head_dim 128, every type at head_dim 256) or a
