@@ -112,16 +112,21 @@ __device__ inline uint32_t bit_range(int lo, int hi) {
   return top & ~((1u << lo) - 1u);
 }
 
-// v where bit i of m is set, +0.0 where it is clear. Bitwise (bit i
-// sign-extended over the word by v_bfe_i32, then AND): two VALU operations
-// and no branch, and a masked value that overflowed to inf still becomes
-// exactly 0. The extract is written as assembly because the compiler
-// rewrites a one-bit sign extension into AND + compare + select (three).
-// i must be a constant once the caller's loops are unrolled (0..31).
-__device__ inline float keep_if_bit(float v, uint32_t m, int i) {
+// Bit i of m sign-extended over a word (all ones or zero): v_bfe_i32,
+// written as assembly because the compiler rewrites a one-bit sign extension
+// into AND + compare + select. i must be a constant once the caller's loops
+// are unrolled (0..31).
+__device__ inline uint32_t bit_sel(uint32_t m, int i) {
   uint32_t sel;
   asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(sel) : "v"(m), "i"(i));
-  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & sel);
+  return sel;
+}
+
+// v where bit i of m is set, +0.0 where it is clear: two VALU operations
+// (extract, AND), no compare or branch, and a masked value that overflowed to
+// inf still becomes exactly 0.
+__device__ inline float keep_if_bit(float v, uint32_t m, int i) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & bit_sel(m, i));
 }
 
 // Workgroups per CU the 256-thread prefill and decode kernels are built for
