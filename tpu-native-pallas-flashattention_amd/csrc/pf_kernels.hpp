@@ -182,7 +182,7 @@ struct DecodeParams {
   const int32_t* context_lens;  // paged: [B] lengths; contiguous: null
   float* part_o;                // [B, Hq, n_split, D] partial (unnormalised) outputs
   float* part_ml;               // [B, Hq, n_split, 2] partial (max, sum)
-  int B, Hq, Hkv, D;  // D: the compute head dim (64 or 128)
+  int B, Hq, Hkv, D;  // D: the compute head dim (64, 128 or, 16-bit, 256)
   // Stored head dim: the row length of q, the cache or pool and o (the
   // generic kernel reads rows of dr elements, dr <= D a multiple of one
   // 16-byte chunk, and treats columns [dr, D) as zeros; the streaming
