@@ -115,7 +115,10 @@ __device__ inline uint32_t bit_range(int lo, int hi) {
 // Bit i of m sign-extended over a word (all ones or zero): v_bfe_i32,
 // written as assembly because the compiler rewrites a one-bit sign extension
 // into AND + compare + select. i must be a constant once the caller's loops
-// are unrolled (0..31).
+// are unrolled (0..31). An ordinary VALU operation on a VGPR that integer
+// VALU code computes (bit_range): none of the hazards the compiler would pad
+// around it (MFMA results, transcendental results, SGPR writes) can reach
+// its operand, so the statement needs no wait states of its own.
 __device__ inline uint32_t bit_sel(uint32_t m, int i) {
   uint32_t sel;
   asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(sel) : "v"(m), "i"(i));
