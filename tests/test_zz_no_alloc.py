@@ -6,7 +6,8 @@ with a caller workspace, on two calls in a row where the second is smaller
 (the array keeps the first call's contents), on the streaming kernel
 (bf16, page 64 and page 16), on a small persistent grid that cuts sequences
 across waves (partials in the array), and on the generic kernel (float32,
-page size 5); sizes past the array are refused before any launch.
+page size 5; bf16 at head_dim 256); sizes past the array are refused before
+any launch.
 A call recorded into a HIP graph replays correctly while its inputs change
 in place, also when it is the process's first call of the entry point (the
 array's address is then looked up during the recording).
@@ -31,7 +32,7 @@ pytestmark = pytest.mark.gpu
 SCRATCH_BYTES = 32 << 20  # PF_NOALLOC_SCRATCH_BYTES
 
 
-def _problem(seed, B, Hq, Hkv, page, pps, num_pages, dt, max_len):
+def _problem(seed, B, Hq, Hkv, page, pps, num_pages, dt, max_len, D=128):
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, max_len + 1, B).astype(np.int32)
     lens[0] = 0  # an empty sequence
@@ -43,9 +44,9 @@ def _problem(seed, B, Hq, Hkv, page, pps, num_pages, dt, max_len):
         table[b, :n] = perm[cur:cur + n]
         cur += n
     assert cur <= num_pages
-    q = dev(rng.standard_normal((B, Hq, 1, 128)), dt)
-    kp = dev(rng.standard_normal((num_pages, Hkv, page, 128)), dt)
-    vp = dev(rng.standard_normal((num_pages, Hkv, page, 128)), dt)
+    q = dev(rng.standard_normal((B, Hq, 1, D)), dt)
+    kp = dev(rng.standard_normal((num_pages, Hkv, page, D)), dt)
+    vp = dev(rng.standard_normal((num_pages, Hkv, page, D)), dt)
     return q, kp, vp, torch.as_tensor(table, device="cuda"), torch.as_tensor(lens, device="cuda")
 
 
@@ -69,21 +70,22 @@ def _with_workspace(L, args, q):
     del ws
 
 
-CASES = [  # (name, dt, page, Hq, Hkv, decode_waves)
-    ("stream bf16 page 64", "bf16", 64, 32, 8, 0),
-    ("stream bf16 page 16, 7-wave grid", "bf16", 16, 16, 2, 7),
-    ("generic f32 page 5", "f32", 5, 8, 2, 0),
+CASES = [  # (name, dt, page, Hq, Hkv, decode_waves, head_dim)
+    ("stream bf16 page 64", "bf16", 64, 32, 8, 0, 128),
+    ("stream bf16 page 16, 7-wave grid", "bf16", 16, 16, 2, 7, 128),
+    ("generic f32 page 5", "f32", 5, 8, 2, 0, 128),
+    ("generic bf16 head_dim 256 page 16", "bf16", 16, 8, 2, 0, 256),
 ]
 
 
-@pytest.mark.parametrize("name,dt,page,Hq,Hkv,waves", CASES)
-def test_noalloc_matches_workspace_entry_point(name, dt, page, Hq, Hkv, waves):
+@pytest.mark.parametrize("name,dt,page,Hq,Hkv,waves,D", CASES)
+def test_noalloc_matches_workspace_entry_point(name, dt, page, Hq, Hkv, waves, D):
     L = _lib.lib()
     stream = torch.cuda.current_stream().cuda_stream
     with _lib.tuning(decode_waves=waves):
         for call, (B, pps, max_len) in enumerate(((24, 40, 40 * page), (5, 12, 12 * page))):
             note(f"noalloc {name}: call {call + 1} B={B} pps={pps}")
-            q, kp, vp, tt, tl = _problem(50 + call, B, Hq, Hkv, page, pps, B * pps, dt, max_len)
+            q, kp, vp, tt, tl = _problem(50 + call, B, Hq, Hkv, page, pps, B * pps, dt, max_len, D)
             want = torch.full_like(q, float("nan"))
             got = torch.full_like(q, float("nan"))
             _with_workspace(L, _args(q, kp, vp, tt, tl, want), q)
