@@ -20,8 +20,10 @@
  *    launch failure is reported as PF_ERR_LAUNCH.
  *  - Thread safety: reentrant. The only state is the process-wide tuning
  *    (pf_set_tuning), a per-device cache of the CU count and kernel
- *    occupancy (filled once per device under std::call_once) and the
- *    per-device scratch array of pf_paged_attn_noalloc (see there).
+ *    occupancy (filled once per device under std::call_once), the per-device
+ *    ticket counters of the prefill kernels' dynamic work tail (one per
+ *    stream, assigned under a mutex; see pf_attn_fwd) and the per-device
+ *    scratch array of pf_paged_attn_noalloc (see there).
  *  - Data types: dtype tags PF_DTYPE_F32 / PF_DTYPE_BF16 / PF_DTYPE_F16 name
  *    the storage type of q/k/v/o (and do/dq/dk/dv); all arithmetic is float32
  *    (MFMA with float32 accumulation). LSE / delta are always float32.
