@@ -309,6 +309,28 @@ void pf_attn_bwd_dq_kernel(BwdParams p, int n_qblk, int n_work) {
 // ---------------------------------------------------------------------------
 // dK / dV (group-summed)
 // ---------------------------------------------------------------------------
+
+// Order of the first S/dP phase of a dK/dV pass: position k of its 2n MFMAs
+// runs S chunk op (op >= 0) or dP chunk -op - 1 (op < 0). The first dly + 1
+// positions are S MFMAs, then the chains alternate, and whichever is left
+// finishes the phase: the dP chain, which starts from -delta read from LDS at
+// the top of the pass, then issues its first MFMA dly + 2 slots after that
+// read instead of one. Each chain keeps its chunk order, so the sums are the
+// same bit for bit.
+__host__ __device__ constexpr int dkv_phase0_op(int k, int n, int dly) {
+  int s = 0, d = 0;
+  for (int pos = 0; pos <= k; ++pos) {
+    bool take_s;
+    if (s == n) take_s = false;
+    else if (d == n) take_s = true;
+    else if (s <= dly) take_s = true;
+    else take_s = (pos - (dly + 1)) % 2 == 1;
+    if (pos == k) return take_s ? s : -(d + 1);
+    if (take_s) ++s;
+    else ++d;
+  }
+  return 0;
+}
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, int n_kblk) {
   using MF = Mfma32<T>;
@@ -571,6 +593,19 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
       // S/dP half 1, dV/dK half 0, dV/dK half 1. Operands are read LEAD MFMAs
       // ahead, across phase boundaries too.
       constexpr int NC = G::CPR / 2, LEAD = 2;
+      // delay of the half-0 dP chain in phase 0 (dkv_phase0_op)
+      constexpr int kDpDelay = 3;
+      // (is dP, chunk) of MFMA k of S/dP phase ph
+      auto sdp_op = [&](int ph, int k, bool& dp, int& ch) __attribute__((always_inline)) {
+        if (ph == 0) {
+          const int op = dkv_phase0_op(k, NC, kDpDelay);
+          dp = op < 0;
+          ch = dp ? -op - 1 : op;
+        } else {
+          dp = (k & 1) != 0;
+          ch = k >> 1;
+        }
+      };
       constexpr int VPS = 16 / NP;  // P/dS values per MFMA slot
       typedef short v4i16 __attribute__((ext_vector_type(4)));
       const int rs0 = mfma_src_row(l32, 0), rs1 = mfma_src_row(l32, 1);
@@ -594,10 +629,14 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
         const int ii = nx ? i - NT : i;
         const int ph = ii / NP, k = ii % NP;
         if (ph < 2) {
-          // S/dP: k even = Q chunk k/2 (S chain), k odd = dO chunk k/2 (dP chain)
+          // S/dP: Q chunk ch (S chain) or dO chunk ch (dP chain), in the
+          // phase's order (sdp_op)
+          bool dp;
+          int ch;
+          sdp_op(ph, k, dp, ch);
           const int r = ph ? rs1 : rs0, sw = ph ? sw1 : sw0;
-          const char* tile = ((k & 1) ? sdo : sq) + (nx ? G::BYTES : 0);
-          opnd[slot] = __builtin_bit_cast(Frag, lds16(tile + r * G::RB + 16 * ((hh * NC + (k >> 1)) ^ sw)));
+          const char* tile = (dp ? sdo : sq) + (nx ? G::BYTES : 0);
+          opnd[slot] = __builtin_bit_cast(Frag, lds16(tile + r * G::RB + 16 * ((hh * NC + ch) ^ sw)));
         } else {
           // dV/dK: k even = dO^T (dV), k odd = Q^T (dK); m = k/2: step 2t + m/NDT, block m%NDT
           const int t = ph - 2, m = k >> 1, c = 2 * t + m / NDT, dt = m % NDT;
@@ -622,8 +661,11 @@ __global__ __launch_bounds__(256, 1) void pf_attn_bwd_dkv_kernel(BwdParams p, in
           if (j + LEAD < NT || U + 1 < NSUB) read(j + LEAD);
           const Frag& a = opnd[(ROFF + j) % (LEAD + 1)];
           if constexpr (ph < 2) {
-            if (k & 1) dx[ph] = MF::run(a, vf[k >> 1], dx[ph]);
-            else sx[ph] = MF::run(a, kf[k >> 1], sx[ph]);
+            bool dp;
+            int ch;
+            sdp_op(ph, k, dp, ch);
+            if (dp) dx[ph] = MF::run(a, vf[ch], dx[ph]);
+            else sx[ph] = MF::run(a, kf[ch], sx[ph]);
             if constexpr (ph == 1 && !kPipe) {
 #pragma unroll
               for (int e = 0; e < VPS; ++e) pds(H0{}, k * VPS + e);
