@@ -123,7 +123,11 @@ def flash_attention_decode_step(
     RoPE at its position, write ``k``/``v`` into the cache slot, and attend
     the single query over the live slots -- ``[0, pos]`` (``ring=False``) or
     the last ``min(pos + 1, capacity)`` tokens of a ring (``ring=True``, slot
-    ``pos % capacity``). The caches are updated in place.
+    ``pos % capacity``). The caches are updated in place. The fused step is
+    the streaming decode kernel's mode for bfloat16/float16 at head_dim 128
+    (the reference model's); other dtypes or head dims raise
+    NotImplementedError -- compose ``write_kv_cache`` (after rotating the
+    new rows) and ``flash_attention_decode`` for them.
 
     Args:
         q: ``[batch, num_heads, 1, head_dim]``, before RoPE.
